@@ -1,0 +1,264 @@
+/*
+ * pss_general.h - the general sampler kernel: one 1024-thread workgroup per
+ * row, exact for every parameter mix and every input distribution (heavy
+ * ties, all-equal rows, +-inf, NaN).  It re-reads the row from memory for each
+ * radix level (8-bit digits, LDS histograms), so it is the correctness
+ * baseline and the fallback of the fast kernel, not the roofline path.
+ *
+ * Semantics per row (reference: shader/Utility/ArgMax-Reduce.comp):
+ *   S0 T <= 0 (or mode GREEDY): argmax of raw logits, smallest id on ties
+ *      (:135-167), position += do_inc, no history / rng change.
+ *   S1/S2 t = l * (1/T); ids in history[0..W) get t = t>0 ? t/rep : t*rep
+ *      (if rep != 1) then t -= pres (:222-265); NaN -> -inf, -0 -> +0.
+ *   S3 tmax = max t.  S4 p = exp(t - tmax), q = trunc(p * 2^45).
+ *   S5 tau_k = K-th largest t (ties kept).   S6 tau_p = largest v with
+ *      sum_{t >= v} q >= ceil(topP * Z_k).   S7 kept: t >= max(tau_k, tau_p)
+ *      and p >= minP.   S8 first kept id (ascending) with cumulative q >
+ *      floor(u24 * Z / 2^24).   S9 epilogue (:376-385).
+ */
+#ifndef PSS_GENERAL_H
+#define PSS_GENERAL_H
+
+#include "pss_device.h"
+
+#define PSS_GEN_NT 1024
+
+/* Row-level epilogue (ArgMax-Reduce.comp:376-385 for sampled rows,
+ * :161-165 for greedy rows).  Called by one thread. */
+__device__ inline void pss_epilogue(const pss_args& a, uint32_t row, uint32_t tok, bool greedy,
+                                    uint32_t W, uint32_t new_rng, pss_row_info inf) {
+    a.result[row * PSS_RESULT_SLOTS + a.pass_idx] = tok;
+    a.token_ids[row] = tok;
+    uint32_t pos = a.position[row];
+    if (!greedy) {
+        if (W > 0u) a.history[row * PSS_MAX_PENALTY_LEN + pos % W] = tok;
+        if (a.rng_mode == PSS_RNG_PHILOX)
+            a.step[row] = a.step[row] + 1u;
+        else
+            a.rng[row] = new_rng;
+    }
+    if (a.do_inc) a.position[row] = pos + 1u;
+    if (a.host_tokens) a.host_tokens[row] = tok;
+    if (a.info) a.info[row] = inf;
+}
+
+/* Uniform of the draw and the rng state after it. */
+__device__ inline uint32_t pss_draw_u24(const pss_args& a, uint32_t row, uint32_t* new_rng) {
+    uint32_t s = a.rng[row];
+    if (a.rng_mode == PSS_RNG_PHILOX) {
+        pss_u32x4 c;
+        c.v[0] = a.step[row];
+        c.v[1] = row;
+        c.v[2] = 0u;
+        c.v[3] = 0u;
+        *new_rng = s;
+        return pss_philox4x32_10(c, s, 0u).v[0] >> 8;
+    }
+    if (s == 0u) s = PSS_XORSHIFT_ZERO_SEED;
+    *new_rng = pss_xorshift32(s);
+    return s >> 8;
+}
+
+struct pss_gen_shared {
+    uint32_t penBits[PSS_MAX_VOCAB / 32];
+    uint64_t hist[256];
+    uint64_t red[PSS_GEN_NT / PSS_WAVE];
+    uint32_t digit;
+    uint64_t rem;
+    uint32_t tok;
+};
+
+__global__ void __launch_bounds__(PSS_GEN_NT) pss_general_kernel(pss_args a) {
+    __shared__ pss_gen_shared sh;
+    constexpr int NT = PSS_GEN_NT;
+    const uint32_t row = blockIdx.x;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t V = a.V;
+    const sample_params sp = a.params[row];
+    const size_t esz = a.dtype == PSS_DTYPE_F16 ? 2u : 4u;
+    const void* rowp = (const char*)a.logits + (size_t)row * a.stride * esz;
+    const bool greedy = (a.mode == PSS_MODE_GREEDY) || !(sp.temperature > 0.0f);
+
+    if (greedy) {
+        uint64_t best = 0;
+        for (uint32_t j = tid; j < V; j += NT) {
+            uint64_t c = ((uint64_t)pss_key(pss_canon(pss_load1(rowp, a.dtype, j))) << 32) |
+                         (uint64_t)(0xFFFFFFFFu - j);
+            best = c > best ? c : best;
+        }
+        best = block_max_u64<NT>(best, sh.red);
+        const uint32_t tok = 0xFFFFFFFFu - (uint32_t)best;
+        if (a.kept_mask)
+            for (uint32_t w = tid; w < a.mask_words; w += NT)
+                a.kept_mask[(size_t)row * a.mask_words + w] =
+                    (w == (tok >> 5)) ? (1u << (tok & 31u)) : 0u;
+        if (a.probs)
+            for (uint32_t j = tid; j < V; j += NT)
+                a.probs[(size_t)row * a.probs_stride + j] = j == tok ? 1.0f : 0.0f;
+        if (tid == 0) {
+            pss_row_info inf = {};
+            inf.token = tok;
+            inf.kept_count = 1;
+            inf.tau_key = (uint32_t)(best >> 32);
+            inf.tmax_key = inf.tau_key;
+            inf.flags = PSS_INFO_GREEDY;
+            pss_epilogue(a, row, tok, true, 0u, 0u, inf);
+        }
+        return;
+    }
+
+    const pss_rowcfg c = pss_make_rowcfg(sp, V);
+    const uint32_t* hist_row = a.history + (size_t)row * PSS_MAX_PENALTY_LEN;
+    if (c.doPen) {
+        const uint32_t words = (V + 31u) / 32u;
+        for (uint32_t i = tid; i < words; i += NT) sh.penBits[i] = 0u;
+        __syncthreads();
+        for (uint32_t h = tid; h < c.W; h += NT) {
+            uint32_t id = hist_row[h];
+            if (id < V) atomicOr(&sh.penBits[id >> 5], 1u << (id & 31u));
+        }
+        __syncthreads();
+    }
+    auto T = [&](uint32_t j) -> float {
+        return pss_transform(pss_load1(rowp, a.dtype, j), c.doPen && pss_bit(sh.penBits, j), c);
+    };
+
+    /* S3 */
+    uint64_t mk = 0;
+    for (uint32_t j = tid; j < V; j += NT) {
+        uint64_t k = pss_key(T(j));
+        mk = k > mk ? k : mk;
+    }
+    const uint32_t tmaxKey = (uint32_t)block_max_u64<NT>(mk, sh.red);
+    const float tmax = pss_unkey(tmaxKey);
+
+    /* Radix select over the row: digit levels of 8 bits from the top.  weight
+     * 0 = count (top-k), 1 = mass restricted to key >= lo (top-p). */
+    auto select = [&](uint64_t rem, int weight, uint32_t lo) -> uint32_t {
+        uint32_t prefix = 0, pmask = 0;
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            for (uint32_t i = tid; i < 256u; i += NT) sh.hist[i] = 0;
+            __syncthreads();
+            for (uint32_t j = tid; j < V; j += NT) {
+                float t = T(j);
+                uint32_t k = pss_key(t);
+                if ((k & pmask) != prefix) continue;
+                if (weight == 0) {
+                    atomicAdd((unsigned long long*)&sh.hist[(k >> shift) & 255u], 1ull);
+                } else if (k >= lo) {
+                    uint64_t q = pss_fixq(pss_prob(t, tmax));
+                    if (q) atomicAdd((unsigned long long*)&sh.hist[(k >> shift) & 255u], (unsigned long long)q);
+                }
+            }
+            __syncthreads();
+            if (tid < 64) wave0_pick_digit(sh.hist, rem, &sh.digit, &sh.rem);
+            __syncthreads();
+            prefix |= sh.digit << shift;
+            pmask |= 0xFFu << shift;
+            rem = sh.rem;
+            __syncthreads();
+        }
+        return prefix;
+    };
+
+    /* S5 */
+    const uint32_t tauK = c.K > 0u ? select(c.K, 0, 0u) : 0u;
+    uint64_t zl = 0;
+    for (uint32_t j = tid; j < V; j += NT) {
+        float t = T(j);
+        if (pss_key(t) >= tauK) zl += pss_fixq(pss_prob(t, tmax));
+    }
+    const uint64_t zk = block_sum_u64<NT>(zl, sh.red);
+    /* S6 */
+    uint32_t tau = tauK;
+    if (c.useTopP) {
+        uint32_t tauP = select(pss_topp_need(c.topP, zk), 1, tauK);
+        tau = tauP > tau ? tauP : tau;
+    }
+
+    /* S7 + S8: per-thread contiguous chunks in id order. */
+    auto kept_q = [&](uint32_t j, uint64_t* q) -> bool {
+        float t = T(j);
+        float p = pss_prob(t, tmax);
+        bool k = pss_key(t) >= tau && (!c.useMinP || p >= c.minP);
+        *q = k ? pss_fixq(p) : 0;
+        return k;
+    };
+    const uint32_t CH = (V + NT - 1u) / NT;
+    const uint32_t j0 = tid * CH < V ? tid * CH : V;
+    const uint32_t j1 = j0 + CH < V ? j0 + CH : V;
+    uint64_t S = 0;
+    uint32_t cnt = 0, lastKept = 0;
+    for (uint32_t j = j0; j < j1; ++j) {
+        uint64_t q;
+        if (kept_q(j, &q)) {
+            S += q;
+            cnt++;
+            lastKept = j + 1u;
+        }
+    }
+    uint64_t Z;
+    const uint64_t P = block_excl_scan_u64<NT>(S, sh.red, &Z);
+    const uint32_t keptCount = (uint32_t)block_sum_u64<NT>(cnt, sh.red);
+    const uint32_t lastAll = (uint32_t)block_max_u64<NT>(lastKept, sh.red);
+    uint32_t newRng;
+    const uint32_t u24 = pss_draw_u24(a, row, &newRng);
+    const uint64_t target = pss_draw_target(u24, Z);
+    if (tid == 0) sh.tok = 0xFFFFFFFFu;
+    __syncthreads();
+    if (S > 0 && P <= target && target < P + S) {
+        uint64_t acc = P;
+        for (uint32_t j = j0; j < j1; ++j) {
+            uint64_t q;
+            if (kept_q(j, &q)) {
+                acc += q;
+                if (acc > target) {
+                    sh.tok = j;
+                    break;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    uint32_t tok = sh.tok;
+    uint32_t flags = 0;
+    if (tok == 0xFFFFFFFFu) {
+        tok = lastAll > 0u ? lastAll - 1u : 0u;
+        flags |= PSS_INFO_FALLBACK;
+    }
+
+    if (a.kept_mask)
+        for (uint32_t w = tid; w < a.mask_words; w += NT) {
+            uint32_t bits = 0;
+            for (uint32_t b = 0; b < 32u; ++b) {
+                uint32_t j = w * 32u + b;
+                uint64_t q;
+                if (j < V && kept_q(j, &q)) bits |= 1u << b;
+            }
+            a.kept_mask[(size_t)row * a.mask_words + w] = bits;
+        }
+    if (a.probs) {
+        const float zf = (float)Z * 0x1.0p-45f;
+        for (uint32_t j = tid; j < V; j += NT) {
+            float t = T(j);
+            float p = pss_prob(t, tmax);
+            bool k = pss_key(t) >= tau && (!c.useMinP || p >= c.minP);
+            a.probs[(size_t)row * a.probs_stride + j] = k ? p / zf : 0.0f;
+        }
+    }
+    if (tid == 0) {
+        pss_row_info inf = {};
+        inf.token = tok;
+        inf.kept_count = keptCount;
+        inf.tau_key = tau;
+        inf.tmax_key = tmaxKey;
+        inf.z_kept = Z;
+        inf.z_topk = zk;
+        inf.target = target;
+        inf.u24 = u24;
+        inf.flags = flags;
+        pss_epilogue(a, row, tok, false, c.W, newRng, inf);
+    }
+}
+
+#endif /* PSS_GENERAL_H */

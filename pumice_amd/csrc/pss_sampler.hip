@@ -1,0 +1,311 @@
+/*
+ * pss_sampler.hip - C ABI of the gfx950 sampler (include/pumice_sampler.h).
+ *
+ * Host side of the drop-in boundary: the sampler object owns the per-row state
+ * buffers that the reference keeps in model_state (src/state.c:84-104:
+ * position, tokenIds, result, sampleParams, sampleRng, sampleHistory), sized for
+ * max_rows independent rows, and enqueues the sampler kernels on one HIP
+ * stream.  Allocation happens only in pss_create.
+ */
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "pss_general.h"
+#include "pss_fast.h"
+#include "pumice_sampler.h"
+
+struct pss_sampler {
+    int device;
+    hipStream_t stream;
+    int own_stream;
+    uint32_t V;
+    uint32_t max_rows;
+    sample_params* d_params;
+    uint32_t* d_rng;
+    uint32_t* d_step;
+    uint32_t* d_pos;
+    uint32_t* d_hist;
+    uint32_t* d_result;
+    uint32_t* d_tokens;
+    void* d_ws;       /* fast-kernel workspace */
+    size_t ws_bytes;
+};
+
+#define HIP_TRY(expr)                            \
+    do {                                         \
+        if ((expr) != hipSuccess) return PSS_ERR_HIP; \
+    } while (0)
+
+extern "C" const char* pss_status_string(pss_status st) {
+    switch (st) {
+        case PSS_OK: return "ok";
+        case PSS_ERR_INVALID_ARG: return "invalid argument";
+        case PSS_ERR_ALLOC: return "allocation failed";
+        case PSS_ERR_HIP: return "HIP runtime error";
+        case PSS_ERR_UNSUPPORTED: return "unsupported";
+        case PSS_ERR_NO_DEVICE: return "no gfx950 device";
+    }
+    return "unknown status";
+}
+
+extern "C" uint32_t pss_mask_words(uint32_t vocab) { return (vocab + 31u) / 32u; }
+
+__global__ void pss_fill_u32_kernel(uint32_t* dst, uint64_t n, uint32_t v) {
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) dst[i] = v;
+}
+
+static pss_status fill_u32(hipStream_t st, uint32_t* dst, uint64_t n, uint32_t v) {
+    if (n == 0) return PSS_OK;
+    uint64_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    pss_fill_u32_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(dst, n, v);
+    return hipGetLastError() == hipSuccess ? PSS_OK : PSS_ERR_HIP;
+}
+
+static void free_all(pss_sampler* s) {
+    if (!s) return;
+    (void)hipFree(s->d_params);
+    (void)hipFree(s->d_rng);
+    (void)hipFree(s->d_step);
+    (void)hipFree(s->d_pos);
+    (void)hipFree(s->d_hist);
+    (void)hipFree(s->d_result);
+    (void)hipFree(s->d_tokens);
+    (void)hipFree(s->d_ws);
+    if (s->own_stream && s->stream) (void)hipStreamDestroy(s->stream);
+    free(s);
+}
+
+extern "C" pss_status pss_create(pss_sampler** out, uint32_t vocab, uint32_t max_rows,
+                                 void* hip_stream) {
+    if (!out) return PSS_ERR_INVALID_ARG;
+    *out = NULL;
+    if (vocab == 0 || max_rows == 0) return PSS_ERR_INVALID_ARG;
+    if (vocab > PSS_MAX_VOCAB) return PSS_ERR_UNSUPPORTED;
+    int dev = 0, ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) return PSS_ERR_NO_DEVICE;
+    if (hipGetDevice(&dev) != hipSuccess) return PSS_ERR_NO_DEVICE;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return PSS_ERR_NO_DEVICE;
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return PSS_ERR_NO_DEVICE;
+
+    pss_sampler* s = (pss_sampler*)calloc(1, sizeof(pss_sampler));
+    if (!s) return PSS_ERR_ALLOC;
+    s->device = dev;
+    s->V = vocab;
+    s->max_rows = max_rows;
+    if (hip_stream) {
+        s->stream = (hipStream_t)hip_stream;
+    } else {
+        if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess) {
+            free(s);
+            return PSS_ERR_HIP;
+        }
+        s->own_stream = 1;
+    }
+    const size_t R = max_rows;
+    s->ws_bytes = pss_fast_ws_bytes(vocab, max_rows);
+    if (hipMalloc((void**)&s->d_params, sizeof(sample_params) * R) != hipSuccess ||
+        hipMalloc((void**)&s->d_rng, 4 * R) != hipSuccess ||
+        hipMalloc((void**)&s->d_step, 4 * R) != hipSuccess ||
+        hipMalloc((void**)&s->d_pos, 4 * R) != hipSuccess ||
+        hipMalloc((void**)&s->d_hist, 4 * R * PSS_MAX_PENALTY_LEN) != hipSuccess ||
+        hipMalloc((void**)&s->d_result, 4 * R * PSS_RESULT_SLOTS) != hipSuccess ||
+        hipMalloc((void**)&s->d_tokens, 4 * R) != hipSuccess ||
+        (s->ws_bytes && hipMalloc(&s->d_ws, s->ws_bytes) != hipSuccess)) {
+        free_all(s);
+        return PSS_ERR_ALLOC;
+    }
+    pss_status st = PSS_OK;
+    if (st == PSS_OK) st = fill_u32(s->stream, (uint32_t*)s->d_params, R * 7, 0u);
+    if (st == PSS_OK) st = fill_u32(s->stream, s->d_rng, R, 0u);
+    if (st == PSS_OK) st = fill_u32(s->stream, s->d_step, R, 0u);
+    if (st == PSS_OK) st = fill_u32(s->stream, s->d_pos, R, 0u);
+    if (st == PSS_OK) st = fill_u32(s->stream, s->d_hist, R * PSS_MAX_PENALTY_LEN, PSS_SENTINEL);
+    if (st == PSS_OK) st = fill_u32(s->stream, s->d_result, R * PSS_RESULT_SLOTS, 0u);
+    if (st == PSS_OK) st = fill_u32(s->stream, s->d_tokens, R, 0u);
+    if (st == PSS_OK && s->ws_bytes) st = fill_u32(s->stream, (uint32_t*)s->d_ws, s->ws_bytes / 4, 0u);
+    if (st == PSS_OK && hipStreamSynchronize(s->stream) != hipSuccess) st = PSS_ERR_HIP;
+    if (st != PSS_OK) {
+        free_all(s);
+        return st;
+    }
+    *out = s;
+    return PSS_OK;
+}
+
+extern "C" pss_status pss_destroy(pss_sampler* s) {
+    if (!s) return PSS_ERR_INVALID_ARG;
+    pss_status st = hipStreamSynchronize(s->stream) == hipSuccess ? PSS_OK : PSS_ERR_HIP;
+    free_all(s);
+    return st;
+}
+
+extern "C" void* pss_stream(pss_sampler* s) { return s ? (void*)s->stream : NULL; }
+
+static int rows_ok(const pss_sampler* s, uint32_t row0, uint32_t rows) {
+    return s && rows > 0 && row0 < s->max_rows && rows <= s->max_rows - row0;
+}
+
+/* Upload `bytes` from host memory and wait for it, so the caller may reuse
+ * the buffer on return (setup path, not the per-step path). */
+static pss_status upload_sync(pss_sampler* s, void* dst, const void* src, size_t bytes) {
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s->stream));
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    return PSS_OK;
+}
+
+extern "C" pss_status pss_set_params(pss_sampler* s, uint32_t row0, uint32_t rows,
+                                     const sample_params* params, const uint32_t* seeds) {
+    if (!rows_ok(s, row0, rows) || !params) return PSS_ERR_INVALID_ARG;
+    for (uint32_t i = 0; i < rows; ++i) {
+        const sample_params& p = params[i];
+        if (isnan(p.topP) || isnan(p.minP) || isnan(p.repPenalty) || isnan(p.presencePenalty))
+            return PSS_ERR_INVALID_ARG;
+        if (p.minP > 1.0f) return PSS_ERR_INVALID_ARG;
+    }
+    pss_status st = upload_sync(s, s->d_params + row0, params, sizeof(sample_params) * rows);
+    if (st != PSS_OK) return st;
+    if (seeds) {
+        st = upload_sync(s, s->d_rng + row0, seeds, 4u * rows);
+    } else {
+        st = fill_u32(s->stream, s->d_rng + row0, rows, 0u);
+    }
+    if (st != PSS_OK) return st;
+    return fill_u32(s->stream, s->d_step + row0, rows, 0u);
+}
+
+extern "C" pss_status pss_reset_history(pss_sampler* s, uint32_t row0, uint32_t rows, uint32_t fill) {
+    if (!rows_ok(s, row0, rows)) return PSS_ERR_INVALID_ARG;
+    return fill_u32(s->stream, s->d_hist + (size_t)row0 * PSS_MAX_PENALTY_LEN,
+                    (uint64_t)rows * PSS_MAX_PENALTY_LEN, fill);
+}
+
+extern "C" pss_status pss_set_history(pss_sampler* s, uint32_t row0, uint32_t rows,
+                                      const uint32_t* hist, uint32_t len) {
+    if (!rows_ok(s, row0, rows) || (!hist && len) || len > PSS_MAX_PENALTY_LEN)
+        return PSS_ERR_INVALID_ARG;
+    size_t n = (size_t)rows * PSS_MAX_PENALTY_LEN;
+    uint32_t* tmp = (uint32_t*)malloc(n * 4);
+    if (!tmp) return PSS_ERR_ALLOC;
+    for (uint32_t r = 0; r < rows; ++r)
+        for (uint32_t h = 0; h < PSS_MAX_PENALTY_LEN; ++h)
+            tmp[(size_t)r * PSS_MAX_PENALTY_LEN + h] = h < len ? hist[(size_t)r * len + h] : PSS_SENTINEL;
+    pss_status st = upload_sync(s, s->d_hist + (size_t)row0 * PSS_MAX_PENALTY_LEN, tmp, n * 4);
+    free(tmp);
+    return st;
+}
+
+extern "C" pss_status pss_set_position(pss_sampler* s, uint32_t row0, uint32_t rows,
+                                       const uint32_t* pos) {
+    if (!rows_ok(s, row0, rows) || !pos) return PSS_ERR_INVALID_ARG;
+    return upload_sync(s, s->d_pos + row0, pos, 4u * rows);
+}
+
+extern "C" pss_status pss_sanitize_request(sample_params* params, uint32_t* seed) {
+    if (!params || !seed) return PSS_ERR_INVALID_ARG;
+    if (params->penaltyLength > PSS_MAX_PENALTY_LEN) params->penaltyLength = PSS_MAX_PENALTY_LEN;
+    if (*seed == 0u) *seed = 1u;
+    return PSS_OK;
+}
+
+static pss_args make_args(pss_sampler* s, const void* logits, uint32_t dtype, uint64_t row_stride,
+                          uint32_t mode, uint32_t do_increment, uint32_t pass_idx,
+                          uint32_t rng_mode, const pss_enqueue_opts* o) {
+    pss_args a;
+    memset(&a, 0, sizeof a);
+    a.logits = logits;
+    a.stride = row_stride;
+    a.V = s->V;
+    a.dtype = dtype;
+    a.mode = mode;
+    a.do_inc = do_increment ? 1u : 0u;
+    a.pass_idx = pass_idx;
+    a.rng_mode = rng_mode;
+    a.params = s->d_params;
+    a.rng = s->d_rng;
+    a.step = s->d_step;
+    a.position = s->d_pos;
+    a.history = s->d_hist;
+    a.result = s->d_result;
+    a.token_ids = s->d_tokens;
+    a.mask_words = pss_mask_words(s->V);
+    a.ws = s->d_ws;
+    if (o) {
+        a.info = o->row_info;
+        a.kept_mask = o->kept_mask;
+        a.probs = o->probs;
+        a.probs_stride = o->probs_stride;
+        a.host_tokens = o->host_tokens;
+    }
+    return a;
+}
+
+extern "C" pss_status pss_enqueue_ex(pss_sampler* s, const void* logits, uint32_t dtype,
+                                     uint64_t row_stride, uint32_t rows, uint32_t mode,
+                                     uint32_t do_increment, uint32_t pass_idx, uint32_t rng_mode,
+                                     const pss_enqueue_opts* opts) {
+    if (!s || !logits || rows == 0 || rows > s->max_rows) return PSS_ERR_INVALID_ARG;
+    if (dtype != PSS_DTYPE_F32 && dtype != PSS_DTYPE_F16) return PSS_ERR_INVALID_ARG;
+    if (mode != PSS_MODE_GREEDY && mode != PSS_MODE_SAMPLE) return PSS_ERR_INVALID_ARG;
+    if (rng_mode != PSS_RNG_XORSHIFT32 && rng_mode != PSS_RNG_PHILOX) return PSS_ERR_INVALID_ARG;
+    if (pass_idx >= PSS_RESULT_SLOTS || row_stride < s->V) return PSS_ERR_INVALID_ARG;
+    if (opts && opts->probs && opts->probs_stride < s->V) return PSS_ERR_INVALID_ARG;
+    pss_args a = make_args(s, logits, dtype, row_stride, mode, do_increment, pass_idx, rng_mode, opts);
+    /* The register-resident fast kernel where it is built for this vocab /
+     * dtype, the general kernel otherwise or when the caller asks for it. */
+    const int general = opts && (opts->flags & PSS_ENQ_GENERAL);
+    if (!general && pss_fast_supported(s->V, dtype, rows)) {
+        if (pss_fast_launch(a, rows, s->stream) != hipSuccess) return PSS_ERR_HIP;
+        return PSS_OK;
+    }
+    pss_general_kernel<<<dim3(rows), dim3(PSS_GEN_NT), 0, s->stream>>>(a);
+    return hipGetLastError() == hipSuccess ? PSS_OK : PSS_ERR_HIP;
+}
+
+extern "C" pss_status pss_enqueue(pss_sampler* s, const void* logits, uint32_t dtype,
+                                  uint64_t row_stride, uint32_t rows, uint32_t mode,
+                                  uint32_t do_increment, uint32_t pass_idx, uint32_t rng_mode) {
+    return pss_enqueue_ex(s, logits, dtype, row_stride, rows, mode, do_increment, pass_idx,
+                          rng_mode, NULL);
+}
+
+extern "C" pss_status pss_read_results(pss_sampler* s, uint32_t rows, uint32_t* results,
+                                       uint32_t* tokens) {
+    if (!s || rows == 0 || rows > s->max_rows) return PSS_ERR_INVALID_ARG;
+    if (results)
+        HIP_TRY(hipMemcpyAsync(results, s->d_result, 4u * PSS_RESULT_SLOTS * rows,
+                               hipMemcpyDeviceToHost, s->stream));
+    if (tokens)
+        HIP_TRY(hipMemcpyAsync(tokens, s->d_tokens, 4u * rows, hipMemcpyDeviceToHost, s->stream));
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    return PSS_OK;
+}
+
+extern "C" pss_status pss_read_state(pss_sampler* s, uint32_t rows, uint32_t* history,
+                                     uint32_t* position, uint32_t* rng, uint32_t* step) {
+    if (!s || rows == 0 || rows > s->max_rows) return PSS_ERR_INVALID_ARG;
+    if (history)
+        HIP_TRY(hipMemcpyAsync(history, s->d_hist, 4u * PSS_MAX_PENALTY_LEN * (size_t)rows,
+                               hipMemcpyDeviceToHost, s->stream));
+    if (position) HIP_TRY(hipMemcpyAsync(position, s->d_pos, 4u * rows, hipMemcpyDeviceToHost, s->stream));
+    if (rng) HIP_TRY(hipMemcpyAsync(rng, s->d_rng, 4u * rows, hipMemcpyDeviceToHost, s->stream));
+    if (step) HIP_TRY(hipMemcpyAsync(step, s->d_step, 4u * rows, hipMemcpyDeviceToHost, s->stream));
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    return PSS_OK;
+}
+
+extern "C" pss_status pss_get_state_ptrs(pss_sampler* s, pss_state_ptrs* out) {
+    if (!s || !out) return PSS_ERR_INVALID_ARG;
+    out->result = s->d_result;
+    out->token_ids = s->d_tokens;
+    out->position = s->d_pos;
+    out->rng = s->d_rng;
+    out->step = s->d_step;
+    out->history = s->d_hist;
+    return PSS_OK;
+}
