@@ -382,3 +382,43 @@ def test_o1_batch_matches_rows_and_threads():
         o = O.o1_row(w.logits[r].astype(np.float32), w.params[r], st, row=r)
         assert o["token"] == int(toks[r])
         assert st.rng == int(rng_s[r]) and np.array_equal(st.history, hist[r])
+
+
+# --------------------------------------------------------------------------
+# committed golden fixtures (tests/golden/make_golden.py)
+# --------------------------------------------------------------------------
+
+def test_validator_golden():
+    with open(os.path.join(GOLDEN, "validator_o1.json")) as f:
+        g = json.load(f)
+    V = g["V"]
+    hist, pos0, cases, seeds = WL.validator_inputs(V)
+    x = O.get_data(777001, 1, V)[0]
+    st = O.RowState(hist, pos0, 0, 0)
+    i = 0
+    for c in range(4):
+        st.rng = int(seeds[c])
+        for d in range(3):
+            o = O.o1_row(x, cases[c], st, want_p=True)
+            exp = g["draws"][i]
+            for f, v in exp["o1"].items():
+                assert int(o["info"][f]) == v, (exp["case"], d, f)
+            assert exp["o3_token"] == o["token"], "O1 and sampler_ref disagree on a validator draw"
+            x = o["p"]
+            i += 1
+    assert st.position == g["final_position"]
+    assert int(st.history.astype(np.uint64).sum()) == g["final_history_sum"]
+
+
+def test_configs_golden():
+    with open(os.path.join(GOLDEN, "configs_o1.json")) as f:
+        g = json.load(f)
+    w, _ = WL.c1(seed=0)
+    assert O.greedy(w.logits[0]) == g["c1_greedy"]
+    st = O.RowState(w.history[0], 0, 0, 0)
+    assert O.o1_row(w.logits[0], w.params[0], st)["token"] == g["c1_sample"]
+    w, xs = WL.c2(seed=24, rows=1, steps=8)
+    st = O.RowState(w.history[0], 0, 99, 0)
+    assert [O.o1_row(xs[k, 0], w.params[0], st)["token"] for k in range(8)] == g["c2_chain"]
+    st = O.RowState(w.history[0], 0, 99, 0)
+    assert [O.o1_row(xs[k, 0], w.params[0], st, rng_mode=1)["token"] for k in range(8)] == g["c2_chain_philox"]
