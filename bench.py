@@ -1,0 +1,242 @@
+#!/usr/bin/env python3
+"""Sampler benchmark on one MI355X: logits -> token, through the C ABI.
+
+A "step" is one pss_enqueue over a batch of logit rows resident in HBM.
+
+  headline  256 x 102,400 fp32 rows, rep 1.1 / presence 0.5 over a 64-id
+            window, T 0.8, top-k 40, top-p 0.95, min-p 0.05  ->  `value` =
+            sampled rows/s, plus algorithmic HBM GB/s and its roofline
+            fraction.  Each step reads a different one of NBUF batches, so the
+            working set (>= 600 MB) exceeds the 256 MB last-level cache and
+            rows come from HBM.
+  latency   batch 1 (config c2): launch-to-token p50/p90 (host clock, token
+            stored by the kernel into pinned host memory), per-step GPU time,
+            and steady decode-group us/token through the C generate loop.
+  c3/c4/c5  the other batched configurations, rows/s and GB/s.
+  cpu_baseline  the O1 oracle (scalar C, sort-based) on the box's host cores
+            over a bounded sample of the headline rows.
+
+Prints ONE JSON line.  Algorithmic bytes per row = V*elem + 4*W + 44.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+NBUF = 6
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def pct(a, q):
+    return float(np.percentile(np.asarray(a), q))
+
+
+def bench_batched(w, steps, warmup, flags=0):
+    """rows/s and per-launch GPU time for workload `w` (rows x V)."""
+    from pumice_amd import hip
+    from pumice_amd import sampler as S
+
+    dtype = S.DTYPE_F16 if w.logits.dtype == np.float16 else S.DTYPE_F32
+    s = S.Sampler(w.V, w.rows)
+    s.set_params(w.params, w.seeds)
+    s.set_history(w.history)
+    bufs = []
+    for b in range(NBUF):
+        bufs.append(hip.DeviceBuffer.from_array(np.roll(w.logits, 977 * b, axis=1)))
+    stream = s.stream
+    for i in range(warmup):
+        s.enqueue(bufs[i % NBUF].ptr, dtype, w.V, w.rows, flags=flags)
+    hip.stream_sync(stream)
+    # timed region: exactly `steps` launches, synchronized on both sides
+    hip.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        s.enqueue(bufs[i % NBUF].ptr, dtype, w.V, w.rows, flags=flags)
+    hip.stream_sync(stream)
+    hip.synchronize()
+    wall = time.perf_counter() - t0
+    # per-launch kernel time with HIP events on the sampler's stream
+    n_ev = min(steps, 100)
+    ev = [(hip.Event(), hip.Event()) for _ in range(n_ev)]
+    for i in range(n_ev):
+        ev[i][0].record(stream)
+        s.enqueue(bufs[i % NBUF].ptr, dtype, w.V, w.rows, flags=flags)
+        ev[i][1].record(stream)
+    hip.stream_sync(stream)
+    kt = [a.elapsed_ms(b) for a, b in ev]
+    res, tok = s.read_results(w.rows)
+    s.close()
+    for b in bufs:
+        b.free()
+    bpr = w.bytes_per_row()
+    k_ms = float(np.mean(kt))
+    return dict(rows=w.rows, V=w.V, dtype=str(w.logits.dtype), ms_per_step=wall * 1e3 / steps,
+                rows_per_s=w.rows * steps / wall, kernel_ms_mean=k_ms, kernel_ms_p50=pct(kt, 50),
+                bytes_per_row=bpr, bytes_per_launch=bpr * w.rows,
+                algo_gbps=bpr * w.rows / (k_ms * 1e-3) / 1e9,
+                wall_gbps=bpr * w.rows * steps / wall / 1e9)
+
+
+def bench_latency(steps):
+    """Batch-1 latency on config c2 with Philox (key 0, counter = step)."""
+    from pumice_amd import generate as G
+    from pumice_amd import hip
+    from pumice_amd import sampler as S
+    from pumice_amd import workloads as WL
+
+    nrows = 64
+    w, xs = WL.c2(seed=2, rows=1, steps=nrows)
+    s = S.Sampler(w.V, 1)
+    s.set_params(w.params, np.zeros(1, np.uint32))
+    s.set_history(w.history)
+    dev = [hip.DeviceBuffer.from_array(xs[k]) for k in range(nrows)]
+    table = G.LogitsTable([d.ptr for d in dev])
+    pinned = hip.PinnedBuffer(64)
+    G.step_latency(s, table, 50, pinned)  # warm
+    lat, toks = G.step_latency(s, table, steps, pinned)
+    # per-step GPU time (events around each launch)
+    stream = s.stream
+    n_ev = min(steps, 200)
+    ev = [(hip.Event(), hip.Event()) for _ in range(n_ev)]
+    for i in range(n_ev):
+        ev[i][0].record(stream)
+        s.enqueue(dev[i % nrows].ptr, S.DTYPE_F32, w.V, 1, rng_mode=S.RNG_PHILOX)
+        ev[i][1].record(stream)
+    hip.stream_sync(stream)
+    gpu_us = [a.elapsed_ms(b) * 1e3 for a, b in ev]
+    # steady decode groups through the C generate loop
+    toks_gen, r = G.generate(s, table, steps, rows=1, rng_mode=S.RNG_PHILOX)
+    s.close()
+    pinned.free()
+    for d in dev:
+        d.free()
+    return dict(steps=steps, launch_to_token_us_p50=pct(lat, 50), launch_to_token_us_p90=pct(lat, 90),
+                gpu_us_p50=pct(gpu_us, 50), gpu_us_p90=pct(gpu_us, 90),
+                decode_group_us_per_token=r["wall_us"] / max(r["emitted"], 1))
+
+
+def cpu_baseline(w, seconds):
+    """O1 (scalar C, sort-based restatement) on a bounded sample of the headline rows."""
+    import oracle as O
+
+    def run(threads):
+        done, t0 = 0, time.perf_counter()
+        while True:
+            hist = w.history.copy()
+            pos = np.zeros(w.rows, np.uint32)
+            rng = w.seeds.copy()
+            step = np.zeros(w.rows, np.uint32)
+            O.o1_batch(w.logits, w.params, hist, pos, rng, step, threads=threads)
+            done += w.rows
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                return done / el, done
+
+    rps1, n1 = run(1)
+    cores = min(16, os.cpu_count() or 1)
+    rpsn, nn = run(cores)
+    return dict(value=rps1, unit="rows/s", cores=1, kind="port",
+                sample=f"{n1} headline rows (256 x 102,400 fp32, c2 chain) in >= {seconds:.0f} s, 1 thread",
+                all_cores=dict(value=rpsn, cores=cores, rows=nn),
+                cpu=_cpu_model())
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--latency-steps", type=int, default=1000)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="headline only (c3/c4/c5 and latency skipped)")
+    ap.add_argument("--general", action="store_true", help="force the general kernel")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(rows shard with no exchange; see the sharding design). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from pumice_amd import sampler as S
+    from pumice_amd import workloads as WL
+
+    flags = S.ENQ_GENERAL if args.general else 0
+    log("generating headline workload")
+    head = WL.headline(seed=0)
+    log("headline: 256 x 102400 fp32")
+    h = bench_batched(head, args.steps, args.warmup, flags)
+    log("headline", json.dumps(h))
+    extra = {}
+    if not args.no_extra:
+        for name, gen in [("c3", lambda: WL.c3(seed=3)), ("c4", lambda: WL.c4(seed=4)),
+                          ("c5", lambda: WL.c5(seed=5))]:
+            log("workload", name)
+            extra[name] = bench_batched(gen(), max(args.steps // 2, 10), args.warmup, flags)
+            log(name, json.dumps(extra[name]))
+        log("latency (batch 1)")
+        extra["latency_b1"] = bench_latency(args.latency_steps)
+        log("latency", json.dumps(extra["latency_b1"]))
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        cpu = cpu_baseline(head, args.cpu_seconds)
+        log("cpu", json.dumps(cpu))
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic_headline.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    achieved = h["algo_gbps"]
+    line = {
+        "metric": "sampled rows/sec + HBM GB/s at V=102,400 (B=256); p50 µs/token at B=1",
+        "value": h["rows_per_s"],
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": h["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded numpy: N(0,3^2) logits, uniform 64-id windows); no dataset",
+        "config": {
+            "workload": "headline: 256 rows x V=102,400 fp32 logits, rep 1.1 + presence 0.5 over a "
+                        "64-id window, T 0.8, top-k 40, top-p 0.95, min-p 0.05, xorshift32 seeds 0..255",
+            "rows": 256, "vocab": 102400, "kernel": "general" if args.general else "auto",
+        },
+        "hbm_gbps": achieved,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic},
+        "cpu_baseline": cpu,
+        "p50_us_per_token_b1": extra.get("latency_b1", {}).get("launch_to_token_us_p50"),
+        "headline": h,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

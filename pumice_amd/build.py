@@ -51,20 +51,24 @@ def _run(cmd, verbose):
 def build(verbose=False):
     """Compile every source into pumice_amd/libpumice_sampler.so (always rebuilds)."""
     objs = []
-    for src in C_SOURCES:
-        path = os.path.join(CSRC, src)
-        if not os.path.exists(path):
-            continue
-        obj = os.path.join(CSRC, src[:-2] + ".o")
-        _run(["gcc", *C_FLAGS, "-I" + INCLUDE, "-I" + CSRC, "-c", path, "-o", obj], verbose)
-        objs.append(obj)
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, *HIP_FLAGS, "-shared", "-I" + INCLUDE, "-I" + CSRC,
-           *[os.path.join(CSRC, s) for s in HIP_SOURCES], *objs, "-o", tmp]
-    _run(cmd, verbose)
-    os.replace(tmp, LIB)
-    for o in objs:
-        os.remove(o)
+    try:
+        for src in C_SOURCES:
+            obj = os.path.join(CSRC, src[:-2] + ".o")
+            _run(["gcc", *C_FLAGS, "-I" + INCLUDE, "-I" + CSRC, "-c", os.path.join(CSRC, src),
+                  "-o", obj], verbose)
+            objs.append(obj)
+        for src in HIP_SOURCES:
+            obj = os.path.join(CSRC, src[:-4] + ".o")
+            _run([HIPCC, *HIP_FLAGS, "-I" + INCLUDE, "-I" + CSRC, "-c", os.path.join(CSRC, src),
+                  "-o", obj], verbose)
+            objs.append(obj)
+        tmp = LIB + ".tmp"
+        _run([HIPCC, "--offload-arch=gfx950", "--hip-link", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
+        os.replace(tmp, LIB)
+    finally:
+        for o in objs:
+            if os.path.exists(o):
+                os.remove(o)
     return LIB
 
 

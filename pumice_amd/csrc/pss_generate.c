@@ -1,0 +1,108 @@
+/*
+ * pss_generate.c - C generate-loop call site of the sampler
+ * (include/pumice_generate.h).  Mirrors the token-consumption structure of
+ * src/generate.c:1027-1159: a prefill-final pass (runPrefill's finalOps,
+ * doIncrement 0, :640-644 / :1009-1016), then decode groups of DECODE_GROUP
+ * passes whose result slots are read back per group (:1118-1156).  Plain C over
+ * the sampler C ABI; no HIP types.
+ */
+#define _POSIX_C_SOURCE 199309L
+#include "pumice_generate.h"
+
+#include <stddef.h>
+#include <time.h>
+
+static double now_us(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec * 1e6 + (double)ts.tv_nsec * 1e-3;
+}
+
+const void* pgl_table_logits(void* ctx, uint32_t position) {
+    const pgl_logits_table* t = (const pgl_logits_table*)ctx;
+    return t->rows[position % t->count];
+}
+
+pss_status pgl_generate(pss_sampler* s, const pgl_config* cfg, pgl_logits_fn logits, void* lctx,
+                        pgl_emit_fn emit, void* ectx, pgl_result* out) {
+    if (!s || !cfg || !logits || !emit || !out || cfg->max_new == 0 || cfg->rows == 0 ||
+        cfg->rows > 256)
+        return PSS_ERR_INVALID_ARG;
+    pgl_result r = {0, 1, 0, 0.0};
+    double t0 = now_us();
+    uint32_t pos = cfg->start_pos;
+    uint32_t results[256 * PGL_DECODE_GROUP];
+    pss_status st;
+
+    /* prefill-final pass: slot 0, no position increment (generate.c:642) */
+    uint32_t posv[256];
+    for (uint32_t i = 0; i < cfg->rows; ++i) posv[i] = pos;
+    st = pss_set_position(s, 0, cfg->rows, posv);
+    if (st != PSS_OK) return st;
+    st = pss_enqueue(s, logits(lctx, pos), cfg->dtype, cfg->row_stride, cfg->rows, cfg->mode, 0, 0,
+                     cfg->rng_mode);
+    if (st != PSS_OK) return st;
+    st = pss_read_results(s, cfg->rows, results, NULL);
+    if (st != PSS_OK) return st;
+    uint32_t tok = results[0];
+    r.emitted = 1;
+    int stop = emit(ectx, tok);
+    if (tok == cfg->eos || stop) {
+        r.finish_reason = 0;
+        r.wall_us = now_us() - t0;
+        *out = r;
+        return PSS_OK;
+    }
+
+    uint32_t remaining = cfg->max_new - 1;
+    while (remaining > 0) {
+        uint32_t cur = remaining < PGL_DECODE_GROUP ? remaining : PGL_DECODE_GROUP;
+        for (uint32_t p = 0; p < cur; ++p) {
+            st = pss_enqueue(s, logits(lctx, pos + p), cfg->dtype, cfg->row_stride, cfg->rows,
+                             cfg->mode, 1, p, cfg->rng_mode);
+            if (st != PSS_OK) return st;
+        }
+        r.groups++;
+        st = pss_read_results(s, cfg->rows, results, NULL);
+        if (st != PSS_OK) return st;
+        pos += cur;
+        for (uint32_t j = 0; j < cur; ++j) {
+            tok = results[j]; /* row 0, slot j */
+            r.emitted++;
+            remaining--;
+            stop = emit(ectx, tok);
+            if (tok == cfg->eos || stop) {
+                r.finish_reason = 0;
+                remaining = 0;
+                break;
+            }
+        }
+    }
+    r.wall_us = now_us() - t0;
+    *out = r;
+    return PSS_OK;
+}
+
+pss_status pgl_step_latency(pss_sampler* s, pgl_logits_fn logits, void* lctx, uint32_t dtype,
+                            uint64_t row_stride, uint32_t rng_mode, uint32_t steps,
+                            uint32_t* pinned_dev, volatile uint32_t* pinned_host, double* lat_us,
+                            uint32_t* tokens) {
+    if (!s || !logits || !pinned_dev || !pinned_host || !lat_us) return PSS_ERR_INVALID_ARG;
+    pss_enqueue_opts o = {NULL, NULL, NULL, 0, pinned_dev, 0};
+    for (uint32_t i = 0; i < steps; ++i) {
+        const void* x = logits(lctx, i);
+        pinned_host[0] = 0xFFFFFFFFu;
+        __atomic_thread_fence(__ATOMIC_SEQ_CST);
+        double t0 = now_us();
+        pss_status st = pss_enqueue_ex(s, x, dtype, row_stride, 1, PSS_MODE_SAMPLE, 1, 0, rng_mode, &o);
+        if (st != PSS_OK) return st;
+        uint32_t v;
+        /* The kernel stores a token < vocab <= 2^18; the sentinel is never a token. */
+        while ((v = __atomic_load_n(pinned_host, __ATOMIC_ACQUIRE)) == 0xFFFFFFFFu) {
+        }
+        lat_us[i] = now_us() - t0;
+        if (tokens) tokens[i] = v;
+    }
+    /* The kernel's remaining state writes are stream-ordered; wait for them. */
+    return pss_read_results(s, 1, NULL, NULL);
+}
