@@ -40,10 +40,9 @@ struct pss_args {
     float* probs;
     uint64_t probs_stride;
     uint32_t* host_tokens;
-    /* multi-segment workspace (fast kernel) */
+    /* per-row workspace of the fast kernel (candidate pools, tickets) */
     void* ws;
-    uint32_t segs;        /* segments per row */
-    uint32_t seg_len;     /* elements per segment */
+    uint32_t vec_ok;      /* rows are 16-byte aligned: vector loads allowed */
 };
 
 /* Per-row sampling constants, derived exactly as ArgMax-Reduce.comp:222-230. */

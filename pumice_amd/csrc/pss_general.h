@@ -1,9 +1,9 @@
 /*
- * pss_general.h - the general sampler kernel: one 1024-thread workgroup per
- * row, exact for every parameter mix and every input distribution (heavy
- * ties, all-equal rows, +-inf, NaN).  It re-reads the row from memory for each
- * radix level (8-bit digits, LDS histograms), so it is the correctness
- * baseline and the fallback of the fast kernel, not the roofline path.
+ * pss_general.h - the general sampler algorithm: one workgroup per row, exact
+ * for every parameter mix and every input distribution (heavy ties, all-equal
+ * rows, +-inf, NaN).  It re-reads the row from memory for each radix level
+ * (8-bit digits, LDS histograms), so it is the correctness baseline and the
+ * in-kernel fallback of the fast kernel, not the roofline path.
  *
  * Semantics per row (reference: shader/Utility/ArgMax-Reduce.comp):
  *   S0 T <= 0 (or mode GREEDY): argmax of raw logits, smallest id on ties
@@ -59,19 +59,41 @@ __device__ inline uint32_t pss_draw_u24(const pss_args& a, uint32_t row, uint32_
     return s >> 8;
 }
 
+/* Greedy outputs of one row (mask / probs / epilogue), `best` = packed
+ * (key << 32) | (0xFFFFFFFF - id) of the argmax. */
+template <int NT>
+__device__ inline void pss_greedy_finish(const pss_args& a, uint32_t row, uint64_t best) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t tok = 0xFFFFFFFFu - (uint32_t)best;
+    if (a.kept_mask)
+        for (uint32_t w = tid; w < a.mask_words; w += NT)
+            a.kept_mask[(size_t)row * a.mask_words + w] = (w == (tok >> 5)) ? (1u << (tok & 31u)) : 0u;
+    if (a.probs)
+        for (uint32_t j = tid; j < a.V; j += NT)
+            a.probs[(size_t)row * a.probs_stride + j] = j == tok ? 1.0f : 0.0f;
+    if (tid == 0) {
+        pss_row_info inf = {};
+        inf.token = tok;
+        inf.kept_count = 1;
+        inf.tau_key = (uint32_t)(best >> 32);
+        inf.tmax_key = inf.tau_key;
+        inf.flags = PSS_INFO_GREEDY;
+        pss_epilogue(a, row, tok, true, 0u, 0u, inf);
+    }
+}
+
+template <int NT>
 struct pss_gen_shared {
     uint32_t penBits[PSS_MAX_VOCAB / 32];
     uint64_t hist[256];
-    uint64_t red[PSS_GEN_NT / PSS_WAVE];
+    uint64_t red[NT / PSS_WAVE];
     uint32_t digit;
     uint64_t rem;
     uint32_t tok;
 };
 
-__global__ void __launch_bounds__(PSS_GEN_NT) pss_general_kernel(pss_args a) {
-    __shared__ pss_gen_shared sh;
-    constexpr int NT = PSS_GEN_NT;
-    const uint32_t row = blockIdx.x;
+template <int NT>
+__device__ void pss_general_row(const pss_args& a, uint32_t row, pss_gen_shared<NT>& sh) {
     const uint32_t tid = threadIdx.x;
     const uint32_t V = a.V;
     const sample_params sp = a.params[row];
@@ -87,23 +109,7 @@ __global__ void __launch_bounds__(PSS_GEN_NT) pss_general_kernel(pss_args a) {
             best = c > best ? c : best;
         }
         best = block_max_u64<NT>(best, sh.red);
-        const uint32_t tok = 0xFFFFFFFFu - (uint32_t)best;
-        if (a.kept_mask)
-            for (uint32_t w = tid; w < a.mask_words; w += NT)
-                a.kept_mask[(size_t)row * a.mask_words + w] =
-                    (w == (tok >> 5)) ? (1u << (tok & 31u)) : 0u;
-        if (a.probs)
-            for (uint32_t j = tid; j < V; j += NT)
-                a.probs[(size_t)row * a.probs_stride + j] = j == tok ? 1.0f : 0.0f;
-        if (tid == 0) {
-            pss_row_info inf = {};
-            inf.token = tok;
-            inf.kept_count = 1;
-            inf.tau_key = (uint32_t)(best >> 32);
-            inf.tmax_key = inf.tau_key;
-            inf.flags = PSS_INFO_GREEDY;
-            pss_epilogue(a, row, tok, true, 0u, 0u, inf);
-        }
+        pss_greedy_finish<NT>(a, row, best);
         return;
     }
 
@@ -259,6 +265,11 @@ __global__ void __launch_bounds__(PSS_GEN_NT) pss_general_kernel(pss_args a) {
         inf.flags = flags;
         pss_epilogue(a, row, tok, false, c.W, newRng, inf);
     }
+}
+
+__global__ void __launch_bounds__(PSS_GEN_NT) pss_general_kernel(pss_args a) {
+    __shared__ pss_gen_shared<PSS_GEN_NT> sh;
+    pss_general_row<PSS_GEN_NT>(a, blockIdx.x, sh);
 }
 
 #endif /* PSS_GENERAL_H */

@@ -93,6 +93,24 @@ def test_c5_adversarial(flags):
              where="c5")
 
 
+FULL_BATCHES = {
+    # name: (generator, rows) -- row counts that select each fast-kernel shape
+    "headline_256x102400_f32": (lambda: WL.headline(seed=31), None),   # 512 x 200, one segment
+    "c3_256x102400_f16": (lambda: WL.c3(seed=32), None),               # 512 x 200, fp16
+    "c5_128x102400_ties": (lambda: WL.c5(seed=33), None),              # 512 x 128, 2 segments
+    "c4_64x248320": (lambda: WL.c4(seed=34), None),                    # 512 x 128, 4 segments
+    "c2_120x65536": (lambda: WL.c2(seed=35, rows=120, V=65536)[0], None),  # 512 x 64, 2 segments
+}
+
+
+@pytest.mark.parametrize("name", sorted(FULL_BATCHES))
+def test_full_batches(name):
+    w = FULL_BATCHES[name][0]()
+    seeds = w.seeds if w.seeds.any() else np.arange(w.rows, dtype=np.uint32) * 7919
+    run_both(w.logits, w.params, seeds, w.history, w.position, steps=2,
+             step_logits=[w.logits, np.roll(w.logits, 1, axis=1)], where=name)
+
+
 @pytest.mark.parametrize("flags", PATHS, ids=PATH_IDS)
 def test_reference_validator_cases(flags):
     """validateArgMaxSampler (src/validation.c:5094-5185): getData(777001) logits,
