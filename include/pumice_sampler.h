@@ -99,8 +99,8 @@ typedef struct {
     uint32_t flags;           /* PSS_ENQ_* bits                                  */
 } pss_enqueue_opts;
 
-/* Run the general multi-pass kernel even where the register-resident fast
- * kernel applies (both compute identical results; used to cross-check them). */
+/* Run the one-workgroup-per-row general kernel instead of the streaming kernel
+ * (both compute identical results; used to cross-check them). */
 #define PSS_ENQ_GENERAL 1u
 
 /* Words per row of kept_mask. */

@@ -1,9 +1,15 @@
 /*
- * pss_general.h - the general sampler algorithm: one workgroup per row, exact
- * for every parameter mix and every input distribution (heavy ties, all-equal
- * rows, +-inf, NaN).  It re-reads the row from memory for each radix level
- * (8-bit digits, LDS histograms), so it is the correctness baseline and the
- * in-kernel fallback of the fast kernel, not the roofline path.
+ * pss_general.h - the general sampler algorithm for one row, run by one
+ * workgroup: exact for every parameter mix and every input distribution
+ * (heavy ties, all-equal rows, +-inf, NaN).  It re-reads the row from memory
+ * for each radix level (8-bit digits, LDS histograms), so it is the
+ * correctness baseline and the in-kernel fallback of the streaming kernel,
+ * not the roofline path.
+ *
+ * The penalty window is an LDS bitmap of `bit_words` words supplied by the
+ * caller.  When it covers the whole vocab it is built once; otherwise every
+ * pass walks the row in chunks of bit_words * 32 ids and rebuilds the bitmap
+ * per chunk, so the fallback fits in a few KB of LDS.
  *
  * Semantics per row (reference: shader/Utility/ArgMax-Reduce.comp):
  *   S0 T <= 0 (or mode GREEDY): argmax of raw logits, smallest id on ties
@@ -22,11 +28,12 @@
 #include "pss_device.h"
 
 #define PSS_GEN_NT 1024
+#define PSS_NO_TOKEN 0xFFFFFFFFu
 
 /* Row-level epilogue (ArgMax-Reduce.comp:376-385 for sampled rows,
  * :161-165 for greedy rows).  Called by one thread. */
-__device__ inline void pss_epilogue(const pss_args& a, uint32_t row, uint32_t tok, bool greedy,
-                                    uint32_t W, uint32_t new_rng, pss_row_info inf) {
+__device__ __forceinline__ void pss_epilogue(const pss_args& a, uint32_t row, uint32_t tok, bool greedy,
+                                    uint32_t W, uint32_t new_rng, const pss_row_info& inf) {
     a.result[row * PSS_RESULT_SLOTS + a.pass_idx] = tok;
     a.token_ids[row] = tok;
     uint32_t pos = a.position[row];
@@ -42,8 +49,44 @@ __device__ inline void pss_epilogue(const pss_args& a, uint32_t row, uint32_t to
     if (a.info) a.info[row] = inf;
 }
 
+/* pss_epilogue with the row's position and Philox step already loaded. */
+__device__ __forceinline__ void pss_epilogue_pre(const pss_args& a, uint32_t row, uint32_t tok, bool greedy,
+                                                 uint32_t W, uint32_t new_rng, const pss_row_info& inf,
+                                                 uint32_t pos, uint32_t step) {
+    a.result[row * PSS_RESULT_SLOTS + a.pass_idx] = tok;
+    a.token_ids[row] = tok;
+    if (!greedy) {
+        if (W > 0u) a.history[row * PSS_MAX_PENALTY_LEN + pos % W] = tok;
+        if (a.rng_mode == PSS_RNG_PHILOX)
+            a.step[row] = step + 1u;
+        else
+            a.rng[row] = new_rng;
+    }
+    if (a.do_inc) a.position[row] = pos + 1u;
+    if (a.host_tokens) a.host_tokens[row] = tok;
+    if (a.info) a.info[row] = inf;
+}
+
+/* Uniform of the draw from the row's rng state s and Philox step, and the
+ * rng state after it. */
+__device__ __forceinline__ uint32_t pss_draw_u24_pre(uint32_t rng_mode, uint32_t s, uint32_t step,
+                                                     uint32_t row, uint32_t* new_rng) {
+    if (rng_mode == PSS_RNG_PHILOX) {
+        pss_u32x4 c;
+        c.v[0] = step;
+        c.v[1] = row;
+        c.v[2] = 0u;
+        c.v[3] = 0u;
+        *new_rng = s;
+        return pss_philox4x32_10(c, s, 0u).v[0] >> 8;
+    }
+    if (s == 0u) s = PSS_XORSHIFT_ZERO_SEED;
+    *new_rng = pss_xorshift32(s);
+    return s >> 8;
+}
+
 /* Uniform of the draw and the rng state after it. */
-__device__ inline uint32_t pss_draw_u24(const pss_args& a, uint32_t row, uint32_t* new_rng) {
+__device__ __forceinline__ uint32_t pss_draw_u24(const pss_args& a, uint32_t row, uint32_t* new_rng) {
     uint32_t s = a.rng[row];
     if (a.rng_mode == PSS_RNG_PHILOX) {
         pss_u32x4 c;
@@ -62,7 +105,7 @@ __device__ inline uint32_t pss_draw_u24(const pss_args& a, uint32_t row, uint32_
 /* Greedy outputs of one row (mask / probs / epilogue), `best` = packed
  * (key << 32) | (0xFFFFFFFF - id) of the argmax. */
 template <int NT>
-__device__ inline void pss_greedy_finish(const pss_args& a, uint32_t row, uint64_t best) {
+__device__ __forceinline__ void pss_greedy_finish(const pss_args& a, uint32_t row, uint64_t best) {
     const uint32_t tid = threadIdx.x;
     const uint32_t tok = 0xFFFFFFFFu - (uint32_t)best;
     if (a.kept_mask)
@@ -82,18 +125,18 @@ __device__ inline void pss_greedy_finish(const pss_args& a, uint32_t row, uint64
     }
 }
 
-template <int NT>
+/* LDS scratch of the general algorithm (besides the penalty bitmap). */
 struct pss_gen_shared {
-    uint32_t penBits[PSS_MAX_VOCAB / 32];
     uint64_t hist[256];
-    uint64_t red[NT / PSS_WAVE];
-    uint32_t digit;
+    uint64_t red[PSS_GEN_NT / PSS_WAVE];
     uint64_t rem;
+    uint32_t digit;
     uint32_t tok;
 };
 
 template <int NT>
-__device__ void pss_general_row(const pss_args& a, uint32_t row, pss_gen_shared<NT>& sh) {
+__device__ __forceinline__ void pss_general_row(const pss_args& a, uint32_t row, pss_gen_shared& sh, uint32_t* bits,
+                                uint32_t bit_words) {
     const uint32_t tid = threadIdx.x;
     const uint32_t V = a.V;
     const sample_params sp = a.params[row];
@@ -115,26 +158,44 @@ __device__ void pss_general_row(const pss_args& a, uint32_t row, pss_gen_shared<
 
     const pss_rowcfg c = pss_make_rowcfg(sp, V);
     const uint32_t* hist_row = a.history + (size_t)row * PSS_MAX_PENALTY_LEN;
-    if (c.doPen) {
-        const uint32_t words = (V + 31u) / 32u;
-        for (uint32_t i = tid; i < words; i += NT) sh.penBits[i] = 0u;
+    const uint32_t CH = bit_words * 32u;
+    const bool chunked = c.doPen && V > CH;
+
+    /* Penalty bitmap of ids [c0, c0 + CH). */
+    auto build = [&](uint32_t c0) {
+        for (uint32_t i = tid; i < bit_words; i += NT) bits[i] = 0u;
         __syncthreads();
         for (uint32_t h = tid; h < c.W; h += NT) {
-            uint32_t id = hist_row[h];
-            if (id < V) atomicOr(&sh.penBits[id >> 5], 1u << (id & 31u));
+            const uint32_t id = hist_row[h];
+            if (id < V && id >= c0 && id - c0 < CH) atomicOr(&bits[(id - c0) >> 5], 1u << ((id - c0) & 31u));
         }
         __syncthreads();
-    }
-    auto T = [&](uint32_t j) -> float {
-        return pss_transform(pss_load1(rowp, a.dtype, j), c.doPen && pss_bit(sh.penBits, j), c);
+    };
+    if (c.doPen && !chunked) build(0u);
+    auto T = [&](uint32_t j, uint32_t c0) -> float {
+        return pss_transform(pss_load1(rowp, a.dtype, j), c.doPen && pss_bit(bits, j - c0), c);
+    };
+    /* One pass over the row: f(j, t) for every id, ids strided over threads.
+     * Every thread of the workgroup calls it. */
+    auto pass = [&](auto&& f) {
+        if (!chunked) {
+            for (uint32_t j = tid; j < V; j += NT) f(j, T(j, 0u));
+            return;
+        }
+        for (uint32_t c0 = 0; c0 < V; c0 += CH) {
+            build(c0);
+            const uint32_t c1 = V - c0 < CH ? V : c0 + CH;
+            for (uint32_t j = c0 + tid; j < c1; j += NT) f(j, T(j, c0));
+            __syncthreads();
+        }
     };
 
     /* S3 */
     uint64_t mk = 0;
-    for (uint32_t j = tid; j < V; j += NT) {
-        uint64_t k = pss_key(T(j));
+    pass([&](uint32_t, float t) {
+        const uint64_t k = pss_key(t);
         mk = k > mk ? k : mk;
-    }
+    });
     const uint32_t tmaxKey = (uint32_t)block_max_u64<NT>(mk, sh.red);
     const float tmax = pss_unkey(tmaxKey);
 
@@ -145,17 +206,16 @@ __device__ void pss_general_row(const pss_args& a, uint32_t row, pss_gen_shared<
         for (int shift = 24; shift >= 0; shift -= 8) {
             for (uint32_t i = tid; i < 256u; i += NT) sh.hist[i] = 0;
             __syncthreads();
-            for (uint32_t j = tid; j < V; j += NT) {
-                float t = T(j);
-                uint32_t k = pss_key(t);
-                if ((k & pmask) != prefix) continue;
+            pass([&](uint32_t, float t) {
+                const uint32_t k = pss_key(t);
+                if ((k & pmask) != prefix) return;
                 if (weight == 0) {
                     atomicAdd((unsigned long long*)&sh.hist[(k >> shift) & 255u], 1ull);
                 } else if (k >= lo) {
-                    uint64_t q = pss_fixq(pss_prob(t, tmax));
+                    const uint64_t q = pss_fixq(pss_prob(t, tmax));
                     if (q) atomicAdd((unsigned long long*)&sh.hist[(k >> shift) & 255u], (unsigned long long)q);
                 }
-            }
+            });
             __syncthreads();
             if (tid < 64) wave0_pick_digit(sh.hist, rem, &sh.digit, &sh.rem);
             __syncthreads();
@@ -170,87 +230,117 @@ __device__ void pss_general_row(const pss_args& a, uint32_t row, pss_gen_shared<
     /* S5 */
     const uint32_t tauK = c.K > 0u ? select(c.K, 0, 0u) : 0u;
     uint64_t zl = 0;
-    for (uint32_t j = tid; j < V; j += NT) {
-        float t = T(j);
+    pass([&](uint32_t, float t) {
         if (pss_key(t) >= tauK) zl += pss_fixq(pss_prob(t, tmax));
-    }
+    });
     const uint64_t zk = block_sum_u64<NT>(zl, sh.red);
     /* S6 */
     uint32_t tau = tauK;
     if (c.useTopP) {
-        uint32_t tauP = select(pss_topp_need(c.topP, zk), 1, tauK);
+        const uint32_t tauP = select(pss_topp_need(c.topP, zk), 1, tauK);
         tau = tauP > tau ? tauP : tau;
     }
 
-    /* S7 + S8: per-thread contiguous chunks in id order. */
-    auto kept_q = [&](uint32_t j, uint64_t* q) -> bool {
-        float t = T(j);
-        float p = pss_prob(t, tmax);
-        bool k = pss_key(t) >= tau && (!c.useMinP || p >= c.minP);
+    /* S7 */
+    auto kept_q = [&](float t, uint64_t* q, float* pout) -> bool {
+        const float p = pss_prob(t, tmax);
+        const bool k = pss_key(t) >= tau && (!c.useMinP || p >= c.minP);
         *q = k ? pss_fixq(p) : 0;
+        *pout = p;
         return k;
     };
-    const uint32_t CH = (V + NT - 1u) / NT;
-    const uint32_t j0 = tid * CH < V ? tid * CH : V;
-    const uint32_t j1 = j0 + CH < V ? j0 + CH : V;
-    uint64_t S = 0;
+    uint64_t zs = 0;
     uint32_t cnt = 0, lastKept = 0;
-    for (uint32_t j = j0; j < j1; ++j) {
+    pass([&](uint32_t j, float t) {
         uint64_t q;
-        if (kept_q(j, &q)) {
-            S += q;
+        float p;
+        if (kept_q(t, &q, &p)) {
+            zs += q;
             cnt++;
             lastKept = j + 1u;
         }
-    }
-    uint64_t Z;
-    const uint64_t P = block_excl_scan_u64<NT>(S, sh.red, &Z);
+    });
+    const uint64_t Z = block_sum_u64<NT>(zs, sh.red);
     const uint32_t keptCount = (uint32_t)block_sum_u64<NT>(cnt, sh.red);
     const uint32_t lastAll = (uint32_t)block_max_u64<NT>(lastKept, sh.red);
+
+    /* S8: walk the row in id order, chunk by chunk; within a chunk each thread
+     * owns a contiguous id range and a block scan orders the ranges. */
     uint32_t newRng;
     const uint32_t u24 = pss_draw_u24(a, row, &newRng);
     const uint64_t target = pss_draw_target(u24, Z);
-    if (tid == 0) sh.tok = 0xFFFFFFFFu;
+    if (tid == 0) sh.tok = PSS_NO_TOKEN;
     __syncthreads();
-    if (S > 0 && P <= target && target < P + S) {
-        uint64_t acc = P;
+    const uint32_t CW = chunked ? CH : V;
+    uint64_t base = 0;
+    for (uint32_t c0 = 0; c0 < V; c0 += CW) {
+        const uint32_t c0b = chunked ? c0 : 0u;
+        if (chunked) build(c0);
+        const uint32_t c1 = V - c0 < CW ? V : c0 + CW;
+        const uint32_t per = (c1 - c0 + NT - 1u) / NT;
+        const uint32_t j0 = c0 + tid * per < c1 ? c0 + tid * per : c1;
+        const uint32_t j1 = j0 + per < c1 ? j0 + per : c1;
+        uint64_t S = 0;
         for (uint32_t j = j0; j < j1; ++j) {
             uint64_t q;
-            if (kept_q(j, &q)) {
-                acc += q;
-                if (acc > target) {
-                    sh.tok = j;
-                    break;
+            float p;
+            if (kept_q(T(j, c0b), &q, &p)) S += q;
+        }
+        uint64_t tot;
+        const uint64_t P = block_excl_scan_u64<NT>(S, sh.red, &tot);
+        if (S > 0 && base + P <= target && target < base + P + S) {
+            uint64_t acc = base + P;
+            for (uint32_t j = j0; j < j1; ++j) {
+                uint64_t q;
+                float p;
+                if (kept_q(T(j, c0b), &q, &p)) {
+                    acc += q;
+                    if (acc > target) {
+                        sh.tok = j;
+                        break;
+                    }
                 }
             }
         }
+        __syncthreads();
+        base += tot;
+        if (sh.tok != PSS_NO_TOKEN || base > target) break;
     }
-    __syncthreads();
     uint32_t tok = sh.tok;
     uint32_t flags = 0;
-    if (tok == 0xFFFFFFFFu) {
+    if (tok == PSS_NO_TOKEN) {
         tok = lastAll > 0u ? lastAll - 1u : 0u;
         flags |= PSS_INFO_FALLBACK;
     }
 
-    if (a.kept_mask)
-        for (uint32_t w = tid; w < a.mask_words; w += NT) {
-            uint32_t bits = 0;
-            for (uint32_t b = 0; b < 32u; ++b) {
-                uint32_t j = w * 32u + b;
-                uint64_t q;
-                if (j < V && kept_q(j, &q)) bits |= 1u << b;
+    /* verification outputs */
+    if (a.kept_mask) {
+        uint32_t* m = a.kept_mask + (size_t)row * a.mask_words;
+        for (uint32_t c0 = 0; c0 < V; c0 += CW) {
+            const uint32_t c0b = chunked ? c0 : 0u;
+            if (chunked) build(c0);
+            const uint32_t c1 = V - c0 < CW ? V : c0 + CW;
+            for (uint32_t w = c0 / 32u + tid; w < (c1 + 31u) / 32u; w += NT) {
+                uint32_t bw = 0;
+                for (uint32_t b = 0; b < 32u; ++b) {
+                    const uint32_t j = w * 32u + b;
+                    uint64_t q;
+                    float p;
+                    if (j < c1 && kept_q(T(j, c0b), &q, &p)) bw |= 1u << b;
+                }
+                m[w] = bw;
             }
-            a.kept_mask[(size_t)row * a.mask_words + w] = bits;
+            if (chunked) __syncthreads();
         }
+    }
     if (a.probs) {
         const float zf = (float)Z * 0x1.0p-45f;
-        for (uint32_t j = tid; j < V; j += NT) {
-            float t = T(j);
-            float p = pss_prob(t, tmax);
-            bool k = pss_key(t) >= tau && (!c.useMinP || p >= c.minP);
-            a.probs[(size_t)row * a.probs_stride + j] = k ? p / zf : 0.0f;
-        }
+        float* pr = a.probs + (size_t)row * a.probs_stride;
+        pass([&](uint32_t j, float t) {
+            uint64_t q;
+            float p;
+            pr[j] = kept_q(t, &q, &p) ? p / zf : 0.0f;
+        });
     }
     if (tid == 0) {
         pss_row_info inf = {};
@@ -267,9 +357,12 @@ __device__ void pss_general_row(const pss_args& a, uint32_t row, pss_gen_shared<
     }
 }
 
+/* One 1024-thread workgroup per row, penalty bitmap over the whole vocab. */
 __global__ void __launch_bounds__(PSS_GEN_NT) pss_general_kernel(pss_args a) {
-    __shared__ pss_gen_shared<PSS_GEN_NT> sh;
-    pss_general_row<PSS_GEN_NT>(a, blockIdx.x, sh);
+    __shared__ pss_gen_shared sh;
+    __shared__ uint32_t bits[PSS_MAX_VOCAB / 32];
+    pss_globalize(a);
+    pss_general_row<PSS_GEN_NT>(a, blockIdx.x, sh, bits, PSS_MAX_VOCAB / 32);
 }
 
 #endif /* PSS_GENERAL_H */

@@ -13,7 +13,7 @@
 #include <string.h>
 
 #include "pss_general.h"
-#include "pss_fast.h"
+#include "pss_stream.h"
 #include "pumice_sampler.h"
 
 struct pss_sampler {
@@ -29,8 +29,9 @@ struct pss_sampler {
     uint32_t* d_hist;
     uint32_t* d_result;
     uint32_t* d_tokens;
-    void* d_ws;       /* fast-kernel workspace */
+    void* d_ws;       /* streaming-kernel workspace: per-row bounds and candidate pools */
     size_t ws_bytes;
+    uint32_t* h_topk; /* host copy of each row's topK (picks the kernel variant) */
 };
 
 #define HIP_TRY(expr)                            \
@@ -76,6 +77,7 @@ static void free_all(pss_sampler* s) {
     (void)hipFree(s->d_result);
     (void)hipFree(s->d_tokens);
     (void)hipFree(s->d_ws);
+    free(s->h_topk);
     if (s->own_stream && s->stream) (void)hipStreamDestroy(s->stream);
     free(s);
 }
@@ -108,7 +110,12 @@ extern "C" pss_status pss_create(pss_sampler** out, uint32_t vocab, uint32_t max
         s->own_stream = 1;
     }
     const size_t R = max_rows;
-    s->ws_bytes = pss_fast_ws_bytes(vocab, max_rows);
+    s->h_topk = (uint32_t*)calloc(R, sizeof(uint32_t));
+    if (!s->h_topk) {
+        free_all(s);
+        return PSS_ERR_ALLOC;
+    }
+    s->ws_bytes = pss_stream_ws_bytes(max_rows);
     if (hipMalloc((void**)&s->d_params, sizeof(sample_params) * R) != hipSuccess ||
         hipMalloc((void**)&s->d_rng, 4 * R) != hipSuccess ||
         hipMalloc((void**)&s->d_step, 4 * R) != hipSuccess ||
@@ -170,6 +177,7 @@ extern "C" pss_status pss_set_params(pss_sampler* s, uint32_t row0, uint32_t row
     }
     pss_status st = upload_sync(s, s->d_params + row0, params, sizeof(sample_params) * rows);
     if (st != PSS_OK) return st;
+    for (uint32_t i = 0; i < rows; ++i) s->h_topk[row0 + i] = params[i].topK;
     if (seeds) {
         st = upload_sync(s, s->d_rng + row0, seeds, 4u * rows);
     } else {
@@ -256,11 +264,13 @@ extern "C" pss_status pss_enqueue_ex(pss_sampler* s, const void* logits, uint32_
     if (pass_idx >= PSS_RESULT_SLOTS || row_stride < s->V) return PSS_ERR_INVALID_ARG;
     if (opts && opts->probs && opts->probs_stride < s->V) return PSS_ERR_INVALID_ARG;
     pss_args a = make_args(s, logits, dtype, row_stride, mode, do_increment, pass_idx, rng_mode, opts);
-    /* The register-resident fast kernel where it is built for this vocab /
-     * dtype, the general kernel otherwise or when the caller asks for it. */
+    /* The streaming kernel, or the one-workgroup-per-row general kernel when
+     * the caller asks for it (both compute identical results). */
     const int general = opts && (opts->flags & PSS_ENQ_GENERAL);
-    if (!general && pss_fast_supported(s->V, dtype, rows)) {
-        if (pss_fast_launch(a, rows, s->stream) != hipSuccess) return PSS_ERR_HIP;
+    if (!general) {
+        uint32_t max_k = 0;
+        for (uint32_t r = 0; r < rows; ++r) max_k = s->h_topk[r] > max_k ? s->h_topk[r] : max_k;
+        if (pss_stream_launch(a, rows, max_k, s->stream) != hipSuccess) return PSS_ERR_HIP;
         return PSS_OK;
     }
     pss_general_kernel<<<dim3(rows), dim3(PSS_GEN_NT), 0, s->stream>>>(a);
