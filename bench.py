@@ -30,6 +30,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
+TRAFFIC_MD = "seg_kernel_traffic_headline.md"
 NBUF = 6
 
 
@@ -39,6 +40,20 @@ def log(*a):
 
 def pct(a, q):
     return float(np.percentile(np.asarray(a), q))
+
+
+def copy_calibration(nbytes, reps=10):
+    """Device-to-device copies of `nbytes` (one logits batch): a kernel of
+    known traffic (nbytes read + nbytes written per dispatch) that scales the
+    FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run."""
+    from pumice_amd import hip
+
+    src, dst = hip.DeviceBuffer(nbytes), hip.DeviceBuffer(nbytes)
+    for _ in range(reps):
+        hip.check(hip.rt().hipMemcpy(dst.ptr, src.ptr, nbytes, hip.hipMemcpyDeviceToDevice), "copy")
+    hip.synchronize()
+    src.free()
+    dst.free()
 
 
 def bench_batched(w, steps, warmup, flags=0):
@@ -65,25 +80,32 @@ def bench_batched(w, steps, warmup, flags=0):
     hip.stream_sync(stream)
     hip.synchronize()
     wall = time.perf_counter() - t0
-    # per-launch kernel time with HIP events on the sampler's stream
+    # per-launch GPU time with HIP events on the sampler's stream: start, the
+    # split event the library records between its two kernels, end
     n_ev = min(steps, 100)
-    ev = [(hip.Event(), hip.Event()) for _ in range(n_ev)]
+    ev = [(hip.Event(), hip.Event(), hip.Event()) for _ in range(n_ev)]
     for i in range(n_ev):
         ev[i][0].record(stream)
-        s.enqueue(bufs[i % NBUF].ptr, dtype, w.V, w.rows, flags=flags)
-        ev[i][1].record(stream)
+        s.enqueue(bufs[i % NBUF].ptr, dtype, w.V, w.rows, flags=flags, split_event=ev[i][1].ptr)
+        ev[i][2].record(stream)
     hip.stream_sync(stream)
-    kt = [a.elapsed_ms(b) for a, b in ev]
+    kt = [a.elapsed_ms(c) for a, b, c in ev]
+    seg = [a.elapsed_ms(b) for a, b, c in ev]
     res, tok = s.read_results(w.rows)
     s.close()
     for b in bufs:
         b.free()
     bpr = w.bytes_per_row()
+    seg_bpr = w.seg_bytes_per_row()
     k_ms = float(np.mean(kt))
+    seg_ms = float(np.mean(seg))
     return dict(rows=w.rows, V=w.V, dtype=str(w.logits.dtype), ms_per_step=wall * 1e3 / steps,
-                rows_per_s=w.rows * steps / wall, kernel_ms_mean=k_ms, kernel_ms_p50=pct(kt, 50),
+                rows_per_s=w.rows * steps / wall, step_ms_mean=k_ms, step_ms_p50=pct(kt, 50),
+                seg_kernel_ms_mean=seg_ms, fin_ms_mean=k_ms - seg_ms,
                 bytes_per_row=bpr, bytes_per_launch=bpr * w.rows,
-                algo_gbps=bpr * w.rows / (k_ms * 1e-3) / 1e9,
+                seg_bytes_per_launch=seg_bpr * w.rows,
+                seg_gbps=seg_bpr * w.rows / (seg_ms * 1e-3) / 1e9,
+                step_gbps=bpr * w.rows / (k_ms * 1e-3) / 1e9,
                 wall_gbps=bpr * w.rows * steps / wall / 1e9)
 
 
@@ -161,6 +183,79 @@ def _cpu_model():
     return "unknown"
 
 
+def traffic_from_pmc(fetch_dir, write_dir, out_path):
+    """HBM bytes per launch of the sampler kernels from two rocprofv3 --pmc runs
+    of `bench.py --no-extra --no-cpu-baseline --copy-calib` (FETCH_SIZE, then
+    WRITE_SIZE; counters in KiB per dispatch).  Each counter is scaled by what it
+    reads for the calibration copy (a device-to-device copy of one headline
+    batch: that many bytes read and written)."""
+    import csv
+    import glob
+
+    def per_kernel(d, counter):
+        files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        vals = {}
+        for fn in files:
+            for r in csv.DictReader(open(fn)):
+                if r["Counter_Name"] == counter:
+                    vals.setdefault((r["Kernel_Name"], int(r["Grid_Size"])), []).append(float(r["Counter_Value"]))
+        return vals
+
+    nbytes = 256 * 102400 * 4
+    out = {}
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        vals = per_kernel(d, counter)
+        copy = [v for (k, g), vs in vals.items() if "copyBuffer" in k for v in vs if v * 1024 > nbytes / 4]
+        if not copy:
+            raise SystemExit(f"{d}: no calibration copy dispatch found")
+        scale = nbytes / (float(np.mean(copy)) * 1024.0)
+        out[counter] = {"copy_kib": float(np.mean(copy)), "scale": scale}
+        for (k, g), vs in vals.items():
+            if k.startswith("void pss_seg_kernel") or k.startswith("pss_fin_kernel"):
+                name = "seg" if "seg_kernel" in k else "fin"
+                out[counter][name + "_kib"] = float(np.mean(vs))
+                out[counter][name + "_bytes"] = float(np.mean(vs)) * 1024.0 * scale
+    seg = out["FETCH_SIZE"]["seg_bytes"] + out["WRITE_SIZE"]["seg_bytes"]
+    fin = out["FETCH_SIZE"]["fin_bytes"] + out["WRITE_SIZE"]["fin_bytes"]
+    res = {"workload": "headline 256 x 102,400 fp32", "calibration_copy_bytes": nbytes,
+           "counters": out, "seg_kernel_hbm_bytes_per_launch": seg, "fin_kernel_hbm_bytes_per_launch": fin,
+           "step_hbm_bytes_per_launch": seg + fin}
+    fc, wc = out["FETCH_SIZE"], out["WRITE_SIZE"]
+    md = [
+        "# HBM traffic of the streaming sampler kernels, headline workload (256 x 102,400 fp32)",
+        "",
+        "Commands (from the repository root on the MI355X box; then, on any host,",
+        "`python3 bench.py --traffic-from <fetch dir> <write dir>` wrote this file):",
+        "",
+        "    cd /tmp && export TMPDIR=/tmp",
+        "    timeout -s KILL 90 rocprofv3 --pmc FETCH_SIZE -d $REPO/gpurun_out/prof_fetch -o run --output-format csv \\",
+        "        -- python3 $REPO/bench.py --no-extra --no-cpu-baseline --steps 10 --warmup 2 --copy-calib",
+        "    timeout -s KILL 90 rocprofv3 --pmc WRITE_SIZE -d $REPO/gpurun_out/prof_write -o run --output-format csv \\",
+        "        -- python3 $REPO/bench.py --no-extra --no-cpu-baseline --steps 10 --warmup 2 --copy-calib",
+        "",
+        "Calibration: a device-to-device copy of one batch (%d bytes read and written) reads"
+        % nbytes,
+        "FETCH_SIZE %.1f KiB and WRITE_SIZE %.1f KiB per dispatch, so the counters are scaled by %.4f and %.4f."
+        % (fc["copy_kib"], wc["copy_kib"], fc["scale"], wc["scale"]),
+        "",
+        "| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes per launch (scaled) |",
+        "|---|---|---|---|",
+        "| pss_seg_kernel | %.1f | %.1f | %.0f |" % (fc["seg_kib"], wc["seg_kib"], seg),
+        "| pss_fin_kernel | %.1f | %.1f | %.0f |" % (fc["fin_kib"], wc["fin_kib"], fin),
+        "",
+        "Algorithmic bytes per launch: segment kernel 256 x (102,400 x 4 + 4 x 64 + 28) = %d;" % (256 * (409600 + 256 + 28)),
+        "whole step 256 x (102,400 x 4 + 4 x 64 + 44) = %d." % (256 * (409600 + 256 + 44)),
+        "",
+        "```json",
+        json.dumps(res, indent=1),
+        "```",
+        "",
+    ]
+    with open(out_path, "w") as f:
+        f.write("\n".join(md))
+    print(json.dumps(res))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -171,7 +266,15 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline only (c3/c4/c5 and latency skipped)")
     ap.add_argument("--general", action="store_true", help="force the general kernel")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="also run device-to-device copies of one headline batch (traffic calibration)")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="no GPU: turn two rocprofv3 --pmc output directories into "
+                         "profiles/traffic_headline.json and exit")
     args = ap.parse_args()
+    if args.traffic_from:
+        traffic_from_pmc(args.traffic_from[0], args.traffic_from[1], os.path.join(ROOT, "profiles", TRAFFIC_MD))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(rows shard with no exchange; see the sharding design). Run with --gpus 1.",
@@ -187,6 +290,9 @@ def main():
     log("headline: 256 x 102400 fp32")
     h = bench_batched(head, args.steps, args.warmup, flags)
     log("headline", json.dumps(h))
+    if args.copy_calib:
+        copy_calibration(head.logits.nbytes)
+        log("copy calibration:", head.logits.nbytes, "bytes per copy")
     extra = {}
     if not args.no_extra:
         for name, gen in [("c3", lambda: WL.c3(seed=3)), ("c4", lambda: WL.c4(seed=4)),
@@ -204,11 +310,14 @@ def main():
         log("cpu", json.dumps(cpu))
 
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "traffic_headline.json")
+    tpath = os.path.join(ROOT, "profiles", TRAFFIC_MD)
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
-    achieved = h["algo_gbps"]
+            txt = f.read()
+        if "```json" in txt:
+            traffic = json.loads(txt.split("```json", 1)[1].split("```", 1)[0]).get(
+                "seg_kernel_hbm_bytes_per_launch")
+    achieved = h["seg_gbps"]
     line = {
         "metric": "sampled rows/sec + HBM GB/s at V=102,400 (B=256); p50 µs/token at B=1",
         "value": h["rows_per_s"],
@@ -227,7 +336,7 @@ def main():
                         "64-id window, T 0.8, top-k 40, top-p 0.95, min-p 0.05, xorshift32 seeds 0..255",
             "rows": 256, "vocab": 102400, "kernel": "general" if args.general else "auto",
         },
-        "hbm_gbps": achieved,
+        "hbm_gbps": h["step_gbps"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic},
         "cpu_baseline": cpu,

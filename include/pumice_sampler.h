@@ -97,6 +97,9 @@ typedef struct {
     uint32_t* host_tokens;    /* device-visible pinned host memory [rows]:
                                  the token of each row is also stored here      */
     uint32_t flags;           /* PSS_ENQ_* bits                                  */
+    void* split_event;        /* hipEvent_t recorded on the sampler's stream after
+                                 the first kernel of the step (per-kernel timing);
+                                 NULL: none                                      */
 } pss_enqueue_opts;
 
 /* Run the one-workgroup-per-row general kernel instead of the streaming kernel

@@ -88,7 +88,7 @@ pss_status pgl_step_latency(pss_sampler* s, pgl_logits_fn logits, void* lctx, ui
                             uint32_t* pinned_dev, volatile uint32_t* pinned_host, double* lat_us,
                             uint32_t* tokens) {
     if (!s || !logits || !pinned_dev || !pinned_host || !lat_us) return PSS_ERR_INVALID_ARG;
-    pss_enqueue_opts o = {NULL, NULL, NULL, 0, pinned_dev, 0};
+    pss_enqueue_opts o = {NULL, NULL, NULL, 0, pinned_dev, 0, NULL};
     for (uint32_t i = 0; i < steps; ++i) {
         const void* x = logits(lctx, i);
         pinned_host[0] = 0xFFFFFFFFu;

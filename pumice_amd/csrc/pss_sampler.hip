@@ -270,11 +270,15 @@ extern "C" pss_status pss_enqueue_ex(pss_sampler* s, const void* logits, uint32_
     if (!general) {
         uint32_t max_k = 0;
         for (uint32_t r = 0; r < rows; ++r) max_k = s->h_topk[r] > max_k ? s->h_topk[r] : max_k;
-        if (pss_stream_launch(a, rows, max_k, s->stream) != hipSuccess) return PSS_ERR_HIP;
+        const hipEvent_t split = opts ? (hipEvent_t)opts->split_event : NULL;
+        if (pss_stream_launch(a, rows, max_k, s->stream, split) != hipSuccess) return PSS_ERR_HIP;
         return PSS_OK;
     }
     pss_general_kernel<<<dim3(rows), dim3(PSS_GEN_NT), 0, s->stream>>>(a);
-    return hipGetLastError() == hipSuccess ? PSS_OK : PSS_ERR_HIP;
+    if (hipGetLastError() != hipSuccess) return PSS_ERR_HIP;
+    if (opts && opts->split_event && hipEventRecord((hipEvent_t)opts->split_event, s->stream) != hipSuccess)
+        return PSS_ERR_HIP;
+    return PSS_OK;
 }
 
 extern "C" pss_status pss_enqueue(pss_sampler* s, const void* logits, uint32_t dtype,

@@ -730,7 +730,8 @@ static inline int pss_stream_pick_ept(uint32_t V, uint32_t rows) {
 }
 
 template <int EPT>
-static inline hipError_t pss_stream_go(const pss_args& a, uint32_t rows, uint32_t max_k, hipStream_t st) {
+static inline hipError_t pss_stream_go(const pss_args& a, uint32_t rows, uint32_t max_k, hipStream_t st,
+                                       hipEvent_t split) {
     const uint32_t seg = (uint32_t)PSS_ST_NT * EPT;
     const uint32_t S = (a.V + seg - 1u) / seg;
     const dim3 grid(S, rows), block(PSS_ST_NT);
@@ -748,18 +749,20 @@ static inline hipError_t pss_stream_go(const pss_args& a, uint32_t rows, uint32_
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (split && (e = hipEventRecord(split, st)) != hipSuccess) return e;
     pss_fin_kernel<<<dim3(rows), dim3(PSS_ST_NT), 0, st>>>(a, S);
     return hipGetLastError();
 }
 
 /* max_k: the largest top-k of the launched rows (an upper bound is enough). */
-static inline hipError_t pss_stream_launch(pss_args a, uint32_t rows, uint32_t max_k, hipStream_t st) {
+static inline hipError_t pss_stream_launch(pss_args a, uint32_t rows, uint32_t max_k, hipStream_t st,
+                                           hipEvent_t split) {
     const size_t esz = a.dtype == PSS_DTYPE_F16 ? 2u : 4u;
     a.vec_ok = ((a.stride * esz) % 16u == 0u) && (((uintptr_t)a.logits & 15u) == 0u);
     switch (pss_stream_pick_ept(a.V, rows)) {
-        case 64: return pss_stream_go<64>(a, rows, max_k, st);
-        case 32: return pss_stream_go<32>(a, rows, max_k, st);
-        default: return pss_stream_go<16>(a, rows, max_k, st);
+        case 64: return pss_stream_go<64>(a, rows, max_k, st, split);
+        case 32: return pss_stream_go<32>(a, rows, max_k, st, split);
+        default: return pss_stream_go<16>(a, rows, max_k, st, split);
     }
 }
 

@@ -53,7 +53,8 @@ class CSampleParams(ctypes.Structure):
 class CEnqueueOpts(ctypes.Structure):
     _fields_ = [("row_info", ctypes.c_void_p), ("kept_mask", ctypes.c_void_p),
                 ("probs", ctypes.c_void_p), ("probs_stride", ctypes.c_uint64),
-                ("host_tokens", ctypes.c_void_p), ("flags", ctypes.c_uint32)]
+                ("host_tokens", ctypes.c_void_p), ("flags", ctypes.c_uint32),
+                ("split_event", ctypes.c_void_p)]
 
 
 class CStatePtrs(ctypes.Structure):
@@ -195,13 +196,15 @@ class Sampler:
 
     def enqueue(self, logits_ptr, dtype, row_stride, rows, mode=MODE_SAMPLE, do_increment=1,
                 pass_idx=0, rng_mode=RNG_XORSHIFT32, row_info=None, kept_mask=None, probs=None,
-                probs_stride=0, host_tokens=None, flags=0):
-        """One step; logits_ptr and the optional outputs are device pointers (ints)."""
-        if row_info is None and kept_mask is None and probs is None and host_tokens is None and not flags:
+                probs_stride=0, host_tokens=None, flags=0, split_event=None):
+        """One step; logits_ptr and the optional outputs are device pointers (ints).
+        split_event: a hipEvent_t recorded between the step's two kernels."""
+        if (row_info is None and kept_mask is None and probs is None and host_tokens is None
+                and not flags and split_event is None):
             st = lib().pss_enqueue(self.handle, logits_ptr, dtype, row_stride, rows, mode,
                                    do_increment, pass_idx, rng_mode)
         else:
-            o = CEnqueueOpts(row_info, kept_mask, probs, probs_stride, host_tokens, flags)
+            o = CEnqueueOpts(row_info, kept_mask, probs, probs_stride, host_tokens, flags, split_event)
             st = lib().pss_enqueue_ex(self.handle, logits_ptr, dtype, row_stride, rows, mode,
                                       do_increment, pass_idx, rng_mode, ctypes.byref(o))
         _ok(st, "pss_enqueue")
