@@ -17,6 +17,15 @@
 
 #define PSS_WAVE 64
 
+/* threadIdx.x behind an empty volatile asm: the value cannot be hoisted out
+ * of a loop, so lane-derived values are recomputed where they are used
+ * instead of holding registers across a persistent kernel's item loop. */
+__device__ __forceinline__ uint32_t pss_tid() {
+    uint32_t t = threadIdx.x;
+    __asm__ __volatile__("" : "+v"(t));
+    return t;
+}
+
 /* Kernel arguments shared by every sampler kernel (passed by value). */
 struct pss_args {
     const void* logits;
@@ -42,7 +51,7 @@ struct pss_args {
     uint32_t* host_tokens;
     /* per-row workspace of the fast kernel (candidate pools, tickets) */
     void* ws;
-    uint32_t vec_ok;      /* rows are 16-byte aligned: vector loads allowed */
+    uint32_t vec_ok;      /* rows 16-byte aligned, V * element size a multiple of 16 */
 };
 
 /* Global-memory pointers.  Pointers that reach a kernel inside a struct are
@@ -153,12 +162,12 @@ __device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
     } else if constexpr (J == 16) {
         /* swap odd rows of the first operand with even rows of the second */
         const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-        return (threadIdx.x & 16u) ? p[0] : p[1];
+        return (pss_tid() & 16u) ? p[0] : p[1];
     } else {
         static_assert(J == 32, "lane_xor: J must be a power of two below 64");
         /* swap the upper half of the first operand with the lower half of the second */
         const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-        return (threadIdx.x & 32u) ? p[0] : p[1];
+        return (pss_tid() & 32u) ? p[0] : p[1];
     }
 }
 
@@ -228,8 +237,58 @@ __device__ __forceinline__ uint64_t dpp_incl_scan_u64(uint64_t x) {
                         (uint32_t)__builtin_amdgcn_readlane(lo, 31);
     const uint64_t r2 = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(hi, 47) << 32) |
                         (uint32_t)__builtin_amdgcn_readlane(lo, 47);
-    const uint32_t rowi = (threadIdx.x >> 4) & 3u;
+    const uint32_t rowi = (pss_tid() >> 4) & 3u;
     return v + (rowi >= 1u ? r0 : 0ull) + (rowi >= 2u ? r1 : 0ull) + (rowi >= 3u ? r2 : 0ull);
+}
+
+/* Inclusive prefix sum of one u32 per lane: row_shr steps within each row
+ * of 16, then the row totals (lanes 15, 31, 47) carried into the rows above. */
+__device__ __forceinline__ uint32_t dpp_incl_scan_u32(uint32_t x) {
+    x += __builtin_amdgcn_update_dpp(0u, x, PSS_DPP_ROW_SHR(1), 0xF, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0u, x, PSS_DPP_ROW_SHR(2), 0xF, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0u, x, PSS_DPP_ROW_SHR(4), 0xF, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0u, x, PSS_DPP_ROW_SHR(8), 0xF, 0xF, false);
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane(x, 15);
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane(x, 31);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane(x, 47);
+    const uint32_t rowi = (pss_tid() >> 4) & 3u;
+    return x + (rowi >= 1u ? r0 : 0u) + (rowi >= 2u ? r1 : 0u) + (rowi >= 3u ? r2 : 0u);
+}
+
+/* One compare-exchange stage (block size KB, distance J) of an ascending
+ * bitonic sort of one u32 per lane. */
+template <int KB, int J>
+__device__ __forceinline__ uint32_t dpp_bitonic_stage_u32(uint32_t x) {
+    const uint32_t y = lane_xor<J>(x);
+    const uint32_t lane = pss_tid() & 63u;
+    const bool lowSide = (lane & (uint32_t)J) == 0u;
+    const bool asc = KB == 64 ? true : (lane & (uint32_t)KB) == 0u;
+    return lowSide == asc ? min(x, y) : max(x, y);
+}
+
+/* Ascending sort of one u32 per lane across the wave. */
+__device__ __forceinline__ uint32_t dpp_sort_asc_u32(uint32_t x) {
+    x = dpp_bitonic_stage_u32<2, 1>(x);
+    x = dpp_bitonic_stage_u32<4, 2>(x);
+    x = dpp_bitonic_stage_u32<4, 1>(x);
+    x = dpp_bitonic_stage_u32<8, 4>(x);
+    x = dpp_bitonic_stage_u32<8, 2>(x);
+    x = dpp_bitonic_stage_u32<8, 1>(x);
+    x = dpp_bitonic_stage_u32<16, 8>(x);
+    x = dpp_bitonic_stage_u32<16, 4>(x);
+    x = dpp_bitonic_stage_u32<16, 2>(x);
+    x = dpp_bitonic_stage_u32<16, 1>(x);
+    x = dpp_bitonic_stage_u32<32, 16>(x);
+    x = dpp_bitonic_stage_u32<32, 8>(x);
+    x = dpp_bitonic_stage_u32<32, 4>(x);
+    x = dpp_bitonic_stage_u32<32, 2>(x);
+    x = dpp_bitonic_stage_u32<32, 1>(x);
+    x = dpp_bitonic_stage_u32<64, 32>(x);
+    x = dpp_bitonic_stage_u32<64, 16>(x);
+    x = dpp_bitonic_stage_u32<64, 8>(x);
+    x = dpp_bitonic_stage_u32<64, 4>(x);
+    x = dpp_bitonic_stage_u32<64, 2>(x);
+    return dpp_bitonic_stage_u32<64, 1>(x);
 }
 
 /* One compare-exchange stage (block size KB, distance J) of an ascending
@@ -237,7 +296,7 @@ __device__ __forceinline__ uint64_t dpp_incl_scan_u64(uint64_t x) {
 template <int KB, int J>
 __device__ __forceinline__ uint64_t dpp_bitonic_stage(uint64_t x) {
     const uint64_t y = lane_xor64<J>(x);
-    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t lane = pss_tid() & 63u;
     const bool lowSide = (lane & (uint32_t)J) == 0u;
     const bool asc = KB == 64 ? true : (lane & (uint32_t)KB) == 0u;
     const uint64_t mn = x < y ? x : y, mx = x < y ? y : x;
@@ -281,7 +340,7 @@ __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) { return (uint32_t)
 
 /* Inclusive prefix sum across the 64 lanes. */
 __device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v) { return dpp_incl_scan_u64(v); }
-__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) { return (uint32_t)dpp_incl_scan_u64(v); }
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) { return dpp_incl_scan_u32(v); }
 
 /* Inclusive suffix sum (sum over lanes >= this lane). */
 __device__ __forceinline__ uint64_t wave_incl_suffix_u64(uint64_t v) {
@@ -299,8 +358,8 @@ template <int NT>
 __device__ inline uint64_t block_sum_u64(uint64_t v, uint64_t* red) {
     constexpr int NW = NT / PSS_WAVE;
     v = wave_sum_u64(v);
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
+    const int w = pss_tid() >> 6;
+    if ((pss_tid() & 63) == 0) red[w] = v;
     __syncthreads();
     uint64_t s = 0;
 #pragma unroll
@@ -313,8 +372,8 @@ template <int NT>
 __device__ inline uint64_t block_max_u64(uint64_t v, uint64_t* red) {
     constexpr int NW = NT / PSS_WAVE;
     v = wave_max_u64(v);
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
+    const int w = pss_tid() >> 6;
+    if ((pss_tid() & 63) == 0) red[w] = v;
     __syncthreads();
     uint64_t s = 0;
 #pragma unroll
@@ -328,8 +387,8 @@ template <int NT>
 __device__ inline uint64_t block_excl_scan_u64(uint64_t v, uint64_t* red, uint64_t* total) {
     constexpr int NW = NT / PSS_WAVE;
     uint64_t inc = wave_incl_scan_u64(v);
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 63) red[w] = inc;
+    const int w = pss_tid() >> 6;
+    if ((pss_tid() & 63) == 63) red[w] = inc;
     __syncthreads();
     uint64_t off = 0, tot = 0;
 #pragma unroll
@@ -350,7 +409,7 @@ __device__ inline uint64_t block_excl_scan_u64(uint64_t v, uint64_t* red, uint64
  */
 __device__ inline void wave0_pick_digit(const uint64_t* hist, uint64_t rem, uint32_t* digit_out,
                                         uint64_t* rem_out) {
-    const int lane = threadIdx.x & 63;
+    const int lane = pss_tid() & 63;
     uint64_t h0 = hist[4 * lane + 0], h1 = hist[4 * lane + 1];
     uint64_t h2 = hist[4 * lane + 2], h3 = hist[4 * lane + 3];
     uint64_t s = h0 + h1 + h2 + h3;
@@ -432,7 +491,7 @@ __device__ __forceinline__ uint64_t wave_read_u64(uint64_t v, uint32_t lane) {
 
 /* Lanes below this one, as a 64-bit mask. */
 __device__ __forceinline__ uint64_t wave_lanes_below() {
-    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t lane = pss_tid() & 63u;
     return lane ? (~0ull >> (64u - lane)) : 0ull;
 }
 

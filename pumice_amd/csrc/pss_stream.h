@@ -408,9 +408,23 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
 /* segment kernel                                                            */
 /* ------------------------------------------------------------------------ */
 
-template <uint32_t SEG>
+template <int EPT, int DT>
+struct pss_seg_geom {
+    static constexpr int E = (DT == PSS_DTYPE_F16) ? 8 : 4; /* elements per 16-byte load */
+    static constexpr int NL = EPT / E;                      /* loads per lane */
+    static constexpr uint32_t SEG = (uint32_t)PSS_ST_NT * EPT;
+    static constexpr int HPT = (int)((PSS_MAX_PENALTY_LEN + PSS_ST_NT - 1) / PSS_ST_NT);
+    static_assert(EPT % E == 0, "EPT must be a multiple of the load width");
+};
+
+/* LDS of a segment workgroup.  The penalty bitmap is transposed: word w is
+ * thread w's, bit i its register t[i]; it and the per-wave bound exchange
+ * are double-buffered (alternating per item that uses them) and cleared by
+ * their readers, so an item needs no barrier before it writes them. */
 struct pss_seg_shared {
-    uint32_t penBits[SEG / 32u];
+    uint32_t pen[2][PSS_ST_NT];          /* window-id bits per thread */
+    uint32_t penOr[2][PSS_SEG_WAVES];    /* OR of the words of each wave */
+    uint32_t lb[2][PSS_SEG_WAVES];       /* per-wave bounds (K <= 256) */
     uint32_t topm[PSS_ST_NT * PSS_TOPM_MAX];
     uint64_t red[PSS_ST_NT / PSS_WAVE];
 };
@@ -421,99 +435,145 @@ struct pss_seg_shared {
 template <int R>
 __device__ __forceinline__ uint32_t pss_lane_bound(const uint32_t* topm, uint32_t K) {
     uint32_t v[R];
-    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t lane = pss_tid() & 63u;
 #pragma unroll
     for (int i = 0; i < R; ++i) v[i] = topm[lane * R + i];
     return wave_kth_largest_r4<R>(v, K, 0u, 31, 16);
 }
 
-/*
- * Segment (seg, row).  FULL: the whole segment lies inside the row and rows
- * are 16-byte aligned, so the loads are issued back to back with no guards
- * (the tail segment and unaligned rows take the guarded path).
- */
-template <int EPT, int DT, bool FULL, bool M1>
-__device__ __forceinline__ void pss_seg_body(const pss_args& a, pss_seg_shared<(uint32_t)PSS_ST_NT * EPT>& sh) {
-    constexpr int NT = PSS_ST_NT;
-    constexpr int E = (DT == PSS_DTYPE_F16) ? 8 : 4; /* elements per 16-byte load */
-    constexpr int NL = EPT / E;
-    constexpr uint32_t SEG = (uint32_t)NT * EPT;
-    constexpr int HPT = (int)((PSS_MAX_PENALTY_LEN + NT - 1) / NT); /* window ids per thread */
-    static_assert(EPT % E == 0, "EPT must be a multiple of the load width");
+/* Row tests from the raw parameters (no division).  A row is covered when
+ * it is greedy or its top-k is on and at most 1024 (otherwise the finisher
+ * runs the general algorithm on it and the segment kernel skips it). */
+__device__ __forceinline__ bool pss_seg_row_greedy(const pss_args& a, const sample_params& sp) {
+    return (a.mode == PSS_MODE_GREEDY) || !(sp.temperature > 0.0f);
+}
+__device__ __forceinline__ bool pss_seg_row_covered(const pss_args& a, const sample_params& sp) {
+    const uint32_t K = sp.topK < a.V ? sp.topK : a.V;
+    return pss_seg_row_greedy(a, sp) || (K > 0u && K <= (uint32_t)PSS_ST_NT * PSS_TOPM_MAX);
+}
 
-    const uint32_t seg = blockIdx.x, row = blockIdx.y, S = gridDim.x;
-    const uint32_t tid = threadIdx.x;
-    const uint32_t V = a.V;
-    const uint32_t seg_base = seg * SEG;
+/* Buffer resource word 3 for raw (untyped, stride 0) buffer loads on gfx9
+ * CDNA parts: 32-bit data format, no swizzle, no index stride. */
+#define PSS_BUF_DW3 0x00020000
 
-    /* 1. The segment's loads go out first: they do not depend on the row's
-     *    parameters. */
-    const size_t esz = DT == PSS_DTYPE_F16 ? 2u : 4u;
+/* Issue the loads of segment `seg` of `row` into raw[]; nothing here waits
+ * for them.  Raw buffer loads over the row (num_records = V * element size):
+ * the hardware returns 0 for ids at or beyond V, which the compute step
+ * replaces by -inf.  vec_ok (16-byte aligned rows, V a multiple of the
+ * elements per 16 bytes): one 16-byte load per 4 fp32 / 8 fp16; otherwise one
+ * load per element. */
+template <int EPT, int DT>
+__device__ __forceinline__ void pss_seg_issue(const pss_args& a, uint32_t row, uint32_t seg,
+                                              uint4 (&raw)[pss_seg_geom<EPT, DT>::NL]) {
+    using Gm = pss_seg_geom<EPT, DT>;
+    constexpr int E = Gm::E, NL = Gm::NL;
+    constexpr uint32_t NT = PSS_ST_NT;
+    constexpr uint32_t esz = DT == PSS_DTYPE_F16 ? 2u : 4u;
+    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
     const char* rowp = (const char*)a.logits + (size_t)row * a.stride * esz;
-    uint4 raw[NL];
-    uint32_t valid[NL];
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)rowp, (short)0, (int)(a.V * esz), PSS_BUF_DW3);
+    const uint32_t tid = pss_tid();
+    const uint32_t base = seg * Gm::SEG;
+    if (a.vec_ok) {
 #pragma unroll
-    for (int li = 0; li < NL; ++li) {
-        const uint32_t j0 = seg_base + (uint32_t)li * (NT * E) + tid * E;
-        if (FULL) {
-            raw[li] = *(const uint4*)(rowp + (size_t)j0 * esz);
-            valid[li] = E;
-        } else if (a.vec_ok && j0 + E <= V) {
-            raw[li] = *(const uint4*)(rowp + (size_t)j0 * esz);
-            valid[li] = E;
-        } else {
+        for (int li = 0; li < NL; ++li) {
+            const v4u v = __builtin_amdgcn_raw_buffer_load_b128(
+                rs, (int)((base + (uint32_t)li * (NT * E) + tid * E) * esz), 0, 0);
+            raw[li] = make_uint4(v.x, v.y, v.z, v.w);
+        }
+    } else {
+#pragma unroll
+        for (int li = 0; li < NL; ++li) {
+            const uint32_t j0 = base + (uint32_t)li * (NT * E) + tid * E;
             uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
             for (int e = 0; e < E; ++e) {
-                if (j0 + e >= V) break;
-                const uint32_t bitsv = DT == PSS_DTYPE_F16 ? (uint32_t)((const uint16_t*)rowp)[j0 + e]
-                                                           : ((const uint32_t*)rowp)[j0 + e];
                 if (DT == PSS_DTYPE_F16)
-                    w[e >> 1] |= bitsv << ((e & 1) * 16);
+                    w[e >> 1] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)((j0 + e) * 2u), 0, 0)
+                                 << ((e & 1) * 16);
                 else
-                    w[e] = bitsv;
+                    w[e] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)((j0 + e) * 4u), 0, 0);
             }
             raw[li] = make_uint4(w[0], w[1], w[2], w[3]);
-            valid[li] = j0 >= V ? 0u : (V - j0 < (uint32_t)E ? V - j0 : (uint32_t)E);
         }
     }
+}
 
-    /* 2. Row parameters (scalar loads), kept behind the segment's loads. */
-    __asm__ __volatile__("" ::: "memory");
-    const sample_params sp = a.params[row];
-    const bool greedy = (a.mode == PSS_MODE_GREEDY) || !(sp.temperature > 0.0f);
-    const pss_rowcfg c = pss_make_rowcfg(sp, V);
-    /* Rows the candidates do not cover are finished by the general
-     * algorithm in the finisher kernel. */
-    if (!greedy && !(c.K > 0u && c.K <= (uint32_t)NT * PSS_TOPM_MAX)) return;
-    pss_row_ws* ws = (pss_row_ws*)((char*)a.ws + (size_t)row * PSS_WS_ROW_BYTES);
-
-    const bool doPen = !greedy && c.doPen;
-    const uint32_t* hist_row = a.history + (size_t)row * PSS_MAX_PENALTY_LEN;
+/* Per-item values loaded ahead of the item: the row's window ids (sampled
+ * rows with a penalty) and the row-wide bound published so far. */
+template <int HPT>
+struct pss_seg_side {
     uint32_t hid[HPT];
+    uint32_t G0;
+};
+
+template <int HPT>
+__device__ __forceinline__ void pss_seg_side_load(const pss_args& a, uint32_t row, const sample_params& sp,
+                                                  pss_seg_side<HPT>& sd) {
+    /* the window ids of sampled rows with a window (a superset of the rows
+     * that apply a penalty; the compute step decides exactly) */
+    const bool greedy = pss_seg_row_greedy(a, sp);
+    const uint32_t W = sp.penaltyLength < PSS_MAX_PENALTY_LEN ? sp.penaltyLength : PSS_MAX_PENALTY_LEN;
+    const uint32_t* hist_row = a.history + (size_t)row * PSS_MAX_PENALTY_LEN;
 #pragma unroll
     for (int h = 0; h < HPT; ++h) {
-        const uint32_t idx = tid + (uint32_t)h * NT;
-        hid[h] = (doPen && idx < c.W) ? hist_row[idx] : PSS_SENTINEL;
+        const uint32_t idx = pss_tid() + (uint32_t)h * PSS_ST_NT;
+        sd.hid[h] = PSS_SENTINEL;
+        if (!greedy && idx < W) sd.hid[h] = hist_row[idx];
     }
-    const uint32_t G0 = greedy ? 0u : pss_ld_agent(&ws->bound);
+    const pss_row_ws* ws = (const pss_row_ws*)((const char*)a.ws + (size_t)row * PSS_WS_ROW_BYTES);
+    /* The lane-varying (zero) offset keeps the value in a vector register:
+     * a uniform load would be moved to a scalar register at once, which
+     * waits for every load issued before it. */
+    uint32_t z = 0u;
+    __asm__ __volatile__("" : "+v"(z));
+    sd.G0 = greedy ? 0u : pss_ld_agent(&ws->bound + z);
+}
 
-    /* 3. Penalty bitmap of this segment's ids. */
-    if (doPen) {
-        for (uint32_t i = tid; i < SEG / 32u; i += NT) sh.penBits[i] = 0u;
-        __syncthreads();
+/* t[i] for a lane-varying index i (a select tree over the bits of i). */
+template <int N>
+__device__ __forceinline__ float pss_pick(const float (&t)[N], uint32_t i) {
+    static_assert((N & (N - 1)) == 0, "power-of-two array");
+    float cur[N];
 #pragma unroll
-        for (int h = 0; h < HPT; ++h) {
-            const uint32_t id = hid[h];
-            if (id >= seg_base && id - seg_base < SEG && id < V) {
-                const uint32_t o = id - seg_base;
-                atomicOr(&sh.penBits[o >> 5], 1u << (o & 31u));
-            }
-        }
-        __syncthreads();
+    for (int k = 0; k < N; ++k) cur[k] = t[k];
+#pragma unroll
+    for (int w = N / 2, bit = 0; w >= 1; w /= 2, ++bit) {
+        const bool hi = (i >> bit) & 1u;
+#pragma unroll
+        for (int k = 0; k < w; ++k) cur[k] = hi ? cur[2 * k + 1] : cur[2 * k];
     }
+    return cur[0];
+}
 
-    /* 4. t = l * (1/T), penalized when in the window (greedy rows: the raw
-     *    logit).  Elements beyond the vocab read as -inf. */
+/*
+ * One segment (seg, row) whose loads are in raw[].  `carry` is the largest
+ * bound this workgroup has established for `carry_row`: every bound is a lower
+ * bound of the row's K-th largest, so later segments of the row reuse it
+ * instead of deriving their own.
+ */
+template <int EPT, int DT, bool M1>
+__device__ __forceinline__ void pss_seg_compute(const pss_args& a, pss_seg_shared& sh, uint32_t row, uint32_t seg,
+                                                uint32_t S, const sample_params& sp,
+                                                const uint4 (&raw)[pss_seg_geom<EPT, DT>::NL],
+                                                const pss_seg_side<pss_seg_geom<EPT, DT>::HPT>& sd,
+                                                uint32_t& carry_row, uint32_t& carry, uint32_t& npen,
+                                                uint32_t& nbound) {
+    using Gm = pss_seg_geom<EPT, DT>;
+    constexpr int NT = PSS_ST_NT;
+    constexpr int E = Gm::E, NL = Gm::NL, HPT = Gm::HPT;
+    constexpr uint32_t SEG = Gm::SEG;
+    static_assert(EPT <= 32, "one bit per register index in a 32-bit word");
+    const uint32_t tid = pss_tid();
+    const uint32_t V = a.V;
+    const uint32_t seg_base = seg * SEG;
+    const bool greedy = pss_seg_row_greedy(a, sp);
+    const pss_rowcfg c = pss_make_rowcfg(sp, V);
+    pss_row_ws* ws = (pss_row_ws*)((char*)a.ws + (size_t)row * PSS_WS_ROW_BYTES);
+    const bool doPen = !greedy && c.doPen;
+
+    /* t = l * (1/T) (greedy rows: the raw logit) */
     const float invT = greedy ? 1.0f : c.invT;
     const float NEG_INF = pss_u2f(0xFF800000u);
     float t[EPT];
@@ -535,115 +595,286 @@ __device__ __forceinline__ void pss_seg_body(const pss_args& a, pss_seg_shared<(
             v[2] = __uint_as_float(raw[li].z);
             v[3] = __uint_as_float(raw[li].w);
         }
-        const uint32_t o = (uint32_t)li * (NT * E) + tid * E;
-        const uint32_t pb = doPen ? (sh.penBits[o >> 5] >> (o & 31u)) & ((1u << E) - 1u) : 0u;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            float x = v[e] * invT;
-            if (pb && ((pb >> e) & 1u)) x = pss_penalize(x, c);
-            t[li * E + e] = (FULL || (uint32_t)e < valid[li]) ? x : NEG_INF;
-        }
+        for (int e = 0; e < E; ++e) t[li * E + e] = v[e] * invT;
     }
-    auto id_of = [&](int i) -> uint32_t {
-        return seg_base + (uint32_t)(i / E) * (NT * E) + tid * E + (uint32_t)(i % E);
+
+    /* Penalty: every thread holding a window id of this segment sets the
+     * owner's bit (element offset o lives in thread (o % (256 E)) / E, register
+     * (o / (256 E)) E + o % E) and the owner wave's summary bit; after one
+     * barrier each thread reads and clears its word, and the wave penalizes
+     * only the register indices some of its lanes hold. */
+    if (doPen) {
+        const uint32_t b = npen & 1u;
+        ++npen;
+#pragma unroll
+        for (int h = 0; h < HPT; ++h) {
+            const uint32_t id = sd.hid[h];
+            if (id >= seg_base && id - seg_base < SEG && id < V) {
+                const uint32_t o = id - seg_base;
+                const uint32_t owner = (o % (uint32_t)(NT * E)) / (uint32_t)E;
+                const uint32_t bit = 1u << ((o / (uint32_t)(NT * E)) * (uint32_t)E + o % (uint32_t)E);
+                atomicOr(&sh.pen[b][owner], bit);
+                atomicOr(&sh.penOr[b][owner >> 6], bit);
+            }
+        }
+        __syncthreads();
+        const uint32_t pb = sh.pen[b][tid];
+        const uint32_t wor = __builtin_amdgcn_readfirstlane(sh.penOr[b][tid >> 6]);
+        sh.pen[b][tid] = 0u;
+        if ((tid & 63u) == 0u) sh.penOr[b][tid >> 6] = 0u;
+#pragma unroll
+        for (int i = 0; i < EPT; ++i)
+            if ((wor >> i) & 1u) t[i] = ((pb >> i) & 1u) ? pss_penalize(t[i], c) : t[i];
+    }
+    auto id_of = [&](uint32_t i) -> uint32_t {
+        return seg_base + (i / E) * (NT * E) + tid * E + (i % E);
     };
-    auto in_vocab = [&](int i) -> bool { return FULL || (uint32_t)(i % E) < valid[i / E]; };
+    /* The row's last segment: ids beyond the vocab read 0; they become -inf,
+     * which never passes a bound above key(-inf) and never wins an argmax
+     * tie against a real id (larger id); where every element passes they are
+     * excluded by id. */
+    if (seg_base + SEG > V) {
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) t[i] = id_of((uint32_t)i) < V ? t[i] : NEG_INF;
+    }
 
     if (greedy) {
         /* argmax of the canonical value, smallest id on ties */
         uint64_t best = 0;
 #pragma unroll
         for (int i = 0; i < EPT; ++i) {
-            const uint64_t b = ((uint64_t)pss_key(pss_canon(t[i])) << 32) | (uint64_t)(0xFFFFFFFFu - id_of(i));
-            if (in_vocab(i) && b > best) best = b;
+            const uint64_t b =
+                ((uint64_t)pss_key(pss_canon(t[i])) << 32) | (uint64_t)(0xFFFFFFFFu - id_of((uint32_t)i));
+            if (b > best) best = b;
         }
         best = block_max_u64<NT>(best, sh.red);
         if (tid == 0) ws->seg_best[seg] = best;
         return;
     }
 
-    /* 5. Bound: per-lane top-m keys to LDS; every wave derives the segment's
-     *    bound from all of them.  max() ignores NaN, which canonicalizes to
-     *    -inf; lanes without elements contribute key(-inf), the smallest key,
-     *    which never raises the bound above a true order statistic. */
-    const uint32_t m = M1 ? 1u : (c.K + NT - 1u) / NT;
-    uint32_t* topm = sh.topm;
-    if (m == 1u) {
-        float mx = NEG_INF;
+    /* Bound (first segment of the row in this workgroup).  max() ignores NaN,
+     * which canonicalizes to -inf; lanes without elements contribute
+     * key(-inf), the smallest key, which never raises the bound above a true
+     * order statistic.
+     *   M1 (K <= 256): every wave sorts its 64 lane maxima; with K' =
+     *   ceil(K / 4), the minimum over the four waves of their K'-th largest
+     *   has at least 4 K' >= K distinct elements of the segment at or above
+     *   it.  Otherwise every lane's sorted top-4 goes to LDS and every wave
+     *   takes the K-th largest of all of them. */
+    uint32_t thr = carry_row == row ? carry : 0u;
+    if (carry_row != row) {
+        uint32_t L;
+        if (M1) {
+            float mx = NEG_INF;
 #pragma unroll
-        for (int i = 0; i < EPT; ++i) mx = fmaxf(mx, t[i]);
-        topm[tid] = pss_key(pss_canon(mx));
-    } else {
-        /* insertion into a sorted top-4 on floats (NaN mapped to -inf first;
-         * -0 and +0 order arbitrarily but share one canonical key) */
-        float t0 = NEG_INF, t1 = NEG_INF, t2 = NEG_INF, t3 = NEG_INF;
+            for (int i = 0; i < EPT; ++i) mx = fmaxf(mx, t[i]);
+            const uint32_t srt = dpp_sort_asc_u32(pss_key(pss_canon(mx)));
+            const uint32_t kq = (c.K + (uint32_t)PSS_SEG_WAVES - 1u) / (uint32_t)PSS_SEG_WAVES;
+            const uint32_t lw = (uint32_t)__builtin_amdgcn_readlane(srt, (int)(64u - kq));
+            const uint32_t b = nbound & 1u;
+            ++nbound;
+            if ((tid & 63u) == 0u) sh.lb[b][tid >> 6] = lw;
+            __syncthreads();
+            L = min(min(sh.lb[b][0], sh.lb[b][1]), min(sh.lb[b][2], sh.lb[b][3]));
+        } else {
+            const uint32_t m = (c.K + NT - 1u) / NT;
+            uint32_t* topm = sh.topm;
+            /* insertion into a sorted top-4 on floats (NaN mapped to -inf
+             * first; -0 and +0 order arbitrarily but share one canonical key) */
+            float t0 = NEG_INF, t1 = NEG_INF, t2 = NEG_INF, t3 = NEG_INF;
 #pragma unroll
-        for (int i = 0; i < EPT; ++i) {
-            float x = fmaxf(t[i], NEG_INF), y;
-            y = fminf(t0, x);
-            t0 = fmaxf(t0, x);
-            x = y;
-            y = fminf(t1, x);
-            t1 = fmaxf(t1, x);
-            x = y;
-            y = fminf(t2, x);
-            t2 = fmaxf(t2, x);
-            x = y;
-            t3 = fmaxf(t3, x);
+            for (int i = 0; i < EPT; ++i) {
+                float x = fmaxf(t[i], NEG_INF), y;
+                y = fminf(t0, x);
+                t0 = fmaxf(t0, x);
+                x = y;
+                y = fminf(t1, x);
+                t1 = fmaxf(t1, x);
+                x = y;
+                y = fminf(t2, x);
+                t2 = fmaxf(t2, x);
+                x = y;
+                t3 = fmaxf(t3, x);
+            }
+            __syncthreads(); /* the previous item's reads of topm are done */
+            topm[tid * m + 0] = pss_key(pss_canon(t0));
+            if (m > 1u) topm[tid * m + 1] = pss_key(pss_canon(t1));
+            if (m > 2u) topm[tid * m + 2] = pss_key(pss_canon(t2));
+            if (m > 3u) topm[tid * m + 3] = pss_key(pss_canon(t3));
+            __syncthreads();
+            if (m == 1u)
+                L = pss_lane_bound<4>(topm, c.K);
+            else if (m == 2u)
+                L = pss_lane_bound<8>(topm, c.K);
+            else if (m == 3u)
+                L = pss_lane_bound<12>(topm, c.K);
+            else
+                L = pss_lane_bound<16>(topm, c.K);
         }
-        topm[tid * m + 0] = pss_key(pss_canon(t0));
-        topm[tid * m + 1] = pss_key(pss_canon(t1));
-        if (m > 2u) topm[tid * m + 2] = pss_key(pss_canon(t2));
-        if (m > 3u) topm[tid * m + 3] = pss_key(pss_canon(t3));
+        thr = L > thr ? L : thr;
     }
-    __syncthreads();
-    uint32_t L;
-    if (m == 1u)
-        L = pss_lane_bound<4>(topm, c.K);
-    else if (m == 2u)
-        L = pss_lane_bound<8>(topm, c.K);
-    else if (m == 3u)
-        L = pss_lane_bound<12>(topm, c.K);
-    else
-        L = pss_lane_bound<16>(topm, c.K);
-    if (tid == 0 && L > PSS_KEY_NEG_INF)
-        (void)__hip_atomic_fetch_max(&ws->bound, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t thr = L > G0 ? L : G0;
+    const uint32_t G0 = __builtin_amdgcn_readfirstlane(sd.G0);
+    if (tid == 0 && thr > G0 && thr > PSS_KEY_NEG_INF)
+        (void)__hip_atomic_fetch_max(&ws->bound, thr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    thr = G0 > thr ? G0 : thr;
+    carry_row = row;
+    carry = thr;
 
-    /* 6. Candidates (key >= thr), written by each wave to its own slot range
-     *    of the pool: count, wave scan, store; no LDS, no barrier.  Above
-     *    key(-inf) the test is a float compare (t >= unkey(thr) is false for
-     *    NaN, which canonicalizes to -inf < thr); at or below it every
-     *    element passes. */
-    const bool all = thr <= PSS_KEY_NEG_INF;
-    const float thr_f = pss_unkey(all ? PSS_KEY_NEG_INF : thr);
-    auto pass = [&](int i) -> bool { return all ? in_vocab(i) : (t[i] >= thr_f); };
-    uint32_t mine = 0;
+    /* Candidates (key >= thr), written by each wave to its own slot range
+     * of the pool: a pass mask per lane, a wave scan of the counts, then each
+     * lane stores its entries (one select tree per entry).  Above key(-inf)
+     * the test is a float compare (t >= unkey(thr) is false for NaN, which
+     * canonicalizes to -inf < thr); at or below it every element of the vocab
+     * passes. */
+    /* bit i of pm: element i passes (built from the top bit down as
+     * pm + pm + pass, a shift-in with no per-bit constants) */
+    uint32_t pm = 0;
+    if (thr <= PSS_KEY_NEG_INF) {
 #pragma unroll
-    for (int i = 0; i < EPT; ++i) mine += pass(i) ? 1u : 0u;
+        for (int i = EPT - 1; i >= 0; --i) pm = pm + pm + (id_of((uint32_t)i) < V ? 1u : 0u);
+    } else {
+        const float thr_f = pss_unkey(thr);
+#pragma unroll
+        for (int i = EPT - 1; i >= 0; --i) pm = pm + pm + (t[i] >= thr_f ? 1u : 0u);
+    }
+    const uint32_t mine = (uint32_t)__popc(pm);
     const uint32_t incl = wave_incl_scan_u32(mine);
     const uint32_t wtot = wave_read_u32(incl, 63);
     const uint32_t slot = seg * PSS_SEG_WAVES + (tid >> 6);
     const uint32_t capw = pss_wave_cap(S);
     if (wtot <= capw) {
         unsigned long long* out = (unsigned long long*)(ws + 1) + (size_t)slot * capw + (incl - mine);
-#pragma unroll
-        for (int i = 0; i < EPT; ++i)
-            if (pass(i)) *out++ = ((unsigned long long)pss_key(pss_canon(t[i])) << 32) | id_of(i);
+        while (pm) {
+            const uint32_t i = (uint32_t)__builtin_ctz(pm);
+            pm &= pm - 1u;
+            *out++ = ((unsigned long long)pss_key(pss_canon(pss_pick(t, i))) << 32) | id_of(i);
+        }
     }
     if ((tid & 63u) == 0u) ws->seg_count[slot] = wtot <= capw ? wtot : PSS_SEG_OVERFLOW;
 }
 
-/* M1: every row of the launch has K <= 256 (one top value per lane); the
- * general form keeps a sorted top-4 per lane, which costs registers. */
+/* Staging area of one workgroup: each wave's 16-byte loads of one item, lane
+ * l of wave w at v[li][w][l] (the layout of a wave's load-to-LDS). */
+template <int EPT, int DT>
+struct pss_seg_stage {
+    uint4 v[pss_seg_geom<EPT, DT>::NL][PSS_SEG_WAVES][PSS_WAVE];
+};
+
+/* Issue item (row, seg)'s 16-byte loads straight into the calling wave's part
+ * of the staging area (raw buffer loads to LDS: no registers held while they
+ * are in flight; 0 for ids at or beyond V).  Requires vec_ok. */
+template <int EPT, int DT>
+__device__ __forceinline__ void pss_seg_issue_lds(const pss_args& a, uint32_t row, uint32_t seg,
+                                                  pss_seg_stage<EPT, DT>& st) {
+    using Gm = pss_seg_geom<EPT, DT>;
+    constexpr int E = Gm::E, NL = Gm::NL;
+    constexpr uint32_t NT = PSS_ST_NT;
+    constexpr uint32_t esz = DT == PSS_DTYPE_F16 ? 2u : 4u;
+    const char* rowp = (const char*)a.logits + (size_t)row * a.stride * esz;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)rowp, (short)0, (int)(a.V * esz), PSS_BUF_DW3);
+    const uint32_t tid = pss_tid();
+    const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t base = seg * Gm::SEG;
+#pragma unroll
+    for (int li = 0; li < NL; ++li)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (__attribute__((address_space(3))) void*)&st.v[li][w][0], 16,
+            (int)((base + (uint32_t)li * (NT * E) + tid * E) * esz), 0, 0, 0);
+}
+
+/*
+ * Persistent segment kernel: item i = (row i / S, segment i % S); workgroup b
+ * processes items [b * per_wg, min((b + 1) * per_wg, n_items)) in order, and
+ * the grid is sized to the resident capacity, so every workgroup runs from
+ * the start.  Pipeline (vec_ok): while item j is computed from registers, item
+ * j + 1's logits stream into the wave's staging area in LDS and its window
+ * ids, row-wide bound and parameters are loaded; at the top of the next
+ * iteration the wave waits for them and moves its staged loads to registers.
+ * Each wave reads back only what its own loads wrote, so the staging area
+ * needs no barrier.  Without vec_ok (unaligned rows, V not a multiple of the
+ * elements per 16 bytes) every item loads element-wise at its own start.  M1:
+ * every row of the launch has K <= 256 (one top value per lane); the general
+ * form keeps a sorted top-4 per lane, which costs registers.  `params` is
+ * a.params as a restrict argument: the workgroup's stores cannot alias it, so
+ * the row parameters of later items still come through scalar loads.
+ */
 template <int EPT, int DT, bool M1>
-__global__ void __launch_bounds__(PSS_ST_NT) pss_seg_kernel(pss_args a) {
-    __shared__ pss_seg_shared<(uint32_t)PSS_ST_NT * EPT> sh;
+__global__ void __launch_bounds__(PSS_ST_NT) pss_seg_kernel(pss_args a, uint32_t S, uint32_t n_items,
+                                                            uint32_t per_wg,
+                                                            const sample_params* __restrict__ params) {
+    using Gm = pss_seg_geom<EPT, DT>;
+    __shared__ pss_seg_shared sh;
+    __shared__ pss_seg_stage<EPT, DT> stage;
     pss_globalize(a);
-    if (a.vec_ok && (blockIdx.x + 1u) * ((uint32_t)PSS_ST_NT * EPT) <= a.V)
-        pss_seg_body<EPT, DT, true, M1>(a, sh);
-    else
-        pss_seg_body<EPT, DT, false, M1>(a, sh);
+    const uint32_t i0 = blockIdx.x * per_wg;
+    const uint32_t i1 = i0 + per_wg < n_items ? i0 + per_wg : n_items;
+    if (i0 >= i1) return;
+    uint32_t n = i1 - i0; /* items left, the current one included */
+    const bool staged = a.vec_ok != 0u;
+
+    uint4 raw[Gm::NL];
+    pss_seg_side<Gm::HPT> sd;
+    uint32_t carry_row = 0xFFFFFFFFu, carry = 0u, npen = 0u, nbound = 0u;
+    auto covered = [&](const sample_params& sp) -> bool { return pss_seg_row_covered(a, sp); };
+    {
+        const uint32_t tid = pss_tid();
+        sh.pen[0][tid] = 0u;
+        sh.pen[1][tid] = 0u;
+        if (tid < 2u * PSS_SEG_WAVES) (&sh.penOr[0][0])[tid] = 0u;
+        __syncthreads();
+    }
+
+    /* (row, seg) and parameters of the current item and the next two */
+    auto advance = [&](uint32_t& r, uint32_t& g) {
+        if (++g == S) {
+            g = 0u;
+            ++r;
+        }
+    };
+    uint32_t row0 = __builtin_amdgcn_readfirstlane(i0 / S);
+    uint32_t seg0 = i0 - row0 * S;
+    uint32_t row1 = row0, seg1 = seg0;
+    advance(row1, seg1);
+    uint32_t row2 = row1, seg2 = seg1;
+    advance(row2, seg2);
+    sample_params sp0 = params[row0];
+    sample_params sp1 = params[n > 1u ? row1 : row0];
+    if (staged) {
+        pss_seg_issue_lds<EPT, DT>(a, row0, seg0, stage);
+        if (covered(sp0)) pss_seg_side_load<Gm::HPT>(a, row0, sp0, sd);
+    }
+    for (;;) {
+        const bool more = n > 1u;
+        if (staged) {
+            pss_wait_mem(); /* this item's staged loads and side values */
+            __asm__ __volatile__("" ::: "memory");
+            const uint32_t tid = pss_tid();
+            const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
+#pragma unroll
+            for (int li = 0; li < Gm::NL; ++li) raw[li] = stage.v[li][w][tid & 63u];
+            pss_wait_mem(); /* the staging area is free again */
+            __asm__ __volatile__("" ::: "memory");
+        } else {
+            pss_seg_issue<EPT, DT>(a, row0, seg0, raw);
+            if (covered(sp0)) pss_seg_side_load<Gm::HPT>(a, row0, sp0, sd);
+        }
+        const pss_seg_side<Gm::HPT> cur = sd;
+        const sample_params sp2 = params[n > 2u ? row2 : row0];
+        if (staged && more) {
+            pss_seg_issue_lds<EPT, DT>(a, row1, seg1, stage);
+            if (covered(sp1)) pss_seg_side_load<Gm::HPT>(a, row1, sp1, sd);
+            __asm__ __volatile__("" ::: "memory");
+        }
+        if (covered(sp0))
+            pss_seg_compute<EPT, DT, M1>(a, sh, row0, seg0, S, sp0, raw, cur, carry_row, carry, npen, nbound);
+        if (!more) break;
+        --n;
+        row0 = row1, seg0 = seg1, sp0 = sp1;
+        row1 = row2, seg1 = seg2, sp1 = sp2;
+        advance(row2, seg2);
+    }
 }
 
 /* ------------------------------------------------------------------------ */
@@ -717,16 +948,41 @@ __global__ void __launch_bounds__(PSS_ST_NT) pss_fin_kernel(pss_args a, uint32_t
 /* host-side launch                                                        */
 /* ---------------------------------------------------------------------- */
 
-/* Elements per lane.  32 (8192-id segments): 63 VGPRs, eight waves per SIMD,
- * and about 50 candidates per segment, so a 102,400-id row gives ~650
- * candidates, inside the fast finisher's 1024.  64 halves the segment count
- * but the doubled register file halves occupancy (measured slower).  16 for
- * vocabularies that would otherwise exceed PSS_SEG_MAX_N segments (none at
- * V <= 262,144) or leave fewer than one workgroup per four CUs. */
+/* Elements per lane: 32 (8192-id segments, one pass bit per element in a
+ * 32-bit mask), or 16 for vocabularies that would otherwise exceed
+ * PSS_SEG_MAX_N segments (none at V <= 262,144) or give fewer than 8 items. */
 static inline int pss_stream_pick_ept(uint32_t V, uint32_t rows) {
     const uint64_t S32 = (V + (uint64_t)PSS_ST_NT * 32u - 1u) / ((uint64_t)PSS_ST_NT * 32u);
     if (S32 > PSS_SEG_MAX_N || (uint64_t)rows * S32 < 8u) return 16;
     return 32;
+}
+
+/* Workgroups of a segment kernel instantiation resident on the current
+ * device at once (occupancy x CUs), cached per device; 0 if unknown. */
+template <int EPT, int DT, bool M1>
+static inline uint32_t pss_seg_capacity() {
+    static uint32_t cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+    if (dev < 64 && cache[dev]) return cache[dev];
+    int cus = 0, nb = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, pss_seg_kernel<EPT, DT, M1>, PSS_ST_NT, 0) !=
+        hipSuccess)
+        return 0;
+    const uint32_t cap = (uint32_t)(nb > 0 ? nb : 1) * (uint32_t)(cus > 0 ? cus : 1);
+    if (dev < 64) cache[dev] = cap;
+    return cap;
+}
+
+template <int EPT, int DT, bool M1>
+static inline hipError_t pss_seg_launch(const pss_args& a, uint32_t S, uint32_t n_items, hipStream_t st) {
+    uint32_t cap = pss_seg_capacity<EPT, DT, M1>();
+    if (cap == 0) cap = n_items;
+    const uint32_t per_wg = (n_items + cap - 1u) / cap;
+    const uint32_t grid = (n_items + per_wg - 1u) / per_wg;
+    pss_seg_kernel<EPT, DT, M1><<<dim3(grid), dim3(PSS_ST_NT), 0, st>>>(a, S, n_items, per_wg, a.params);
+    return hipGetLastError();
 }
 
 template <int EPT>
@@ -734,20 +990,16 @@ static inline hipError_t pss_stream_go(const pss_args& a, uint32_t rows, uint32_
                                        hipEvent_t split) {
     const uint32_t seg = (uint32_t)PSS_ST_NT * EPT;
     const uint32_t S = (a.V + seg - 1u) / seg;
-    const dim3 grid(S, rows), block(PSS_ST_NT);
+    if ((uint64_t)rows * S >= (1ull << 31)) return hipErrorInvalidValue;
+    const uint32_t n_items = rows * S;
     const bool m1 = max_k <= (uint32_t)PSS_ST_NT;
-    if (a.dtype == PSS_DTYPE_F16) {
-        if (m1)
-            pss_seg_kernel<EPT, PSS_DTYPE_F16, true><<<grid, block, 0, st>>>(a);
-        else
-            pss_seg_kernel<EPT, PSS_DTYPE_F16, false><<<grid, block, 0, st>>>(a);
-    } else {
-        if (m1)
-            pss_seg_kernel<EPT, PSS_DTYPE_F32, true><<<grid, block, 0, st>>>(a);
-        else
-            pss_seg_kernel<EPT, PSS_DTYPE_F32, false><<<grid, block, 0, st>>>(a);
-    }
-    hipError_t e = hipGetLastError();
+    hipError_t e;
+    if (a.dtype == PSS_DTYPE_F16)
+        e = m1 ? pss_seg_launch<EPT, PSS_DTYPE_F16, true>(a, S, n_items, st)
+               : pss_seg_launch<EPT, PSS_DTYPE_F16, false>(a, S, n_items, st);
+    else
+        e = m1 ? pss_seg_launch<EPT, PSS_DTYPE_F32, true>(a, S, n_items, st)
+               : pss_seg_launch<EPT, PSS_DTYPE_F32, false>(a, S, n_items, st);
     if (e != hipSuccess) return e;
     if (split && (e = hipEventRecord(split, st)) != hipSuccess) return e;
     pss_fin_kernel<<<dim3(rows), dim3(PSS_ST_NT), 0, st>>>(a, S);
@@ -758,9 +1010,9 @@ static inline hipError_t pss_stream_go(const pss_args& a, uint32_t rows, uint32_
 static inline hipError_t pss_stream_launch(pss_args a, uint32_t rows, uint32_t max_k, hipStream_t st,
                                            hipEvent_t split) {
     const size_t esz = a.dtype == PSS_DTYPE_F16 ? 2u : 4u;
-    a.vec_ok = ((a.stride * esz) % 16u == 0u) && (((uintptr_t)a.logits & 15u) == 0u);
+    a.vec_ok = ((a.stride * esz) % 16u == 0u) && (((uintptr_t)a.logits & 15u) == 0u) &&
+               ((a.V * esz) % 16u == 0u);
     switch (pss_stream_pick_ept(a.V, rows)) {
-        case 64: return pss_stream_go<64>(a, rows, max_k, st, split);
         case 32: return pss_stream_go<32>(a, rows, max_k, st, split);
         default: return pss_stream_go<16>(a, rows, max_k, st, split);
     }
