@@ -98,13 +98,17 @@ typedef struct {
                                  the token of each row is also stored here      */
     uint32_t flags;           /* PSS_ENQ_* bits                                  */
     void* split_event;        /* hipEvent_t recorded on the sampler's stream after
-                                 the first kernel of the step (per-kernel timing);
-                                 NULL: none                                      */
+                                 the first kernel of the step (with PSS_ENQ_SPLIT:
+                                 per-kernel timing); NULL: none                  */
 } pss_enqueue_opts;
 
 /* Run the one-workgroup-per-row general kernel instead of the streaming kernel
  * (both compute identical results; used to cross-check them). */
 #define PSS_ENQ_GENERAL 1u
+/* Run the streaming path as two kernels (segment kernel over all rows, then a
+ * finisher kernel per row) instead of the fused one-workgroup-per-row kernel
+ * (identical results; used to cross-check them). */
+#define PSS_ENQ_SPLIT 2u
 
 /* Words per row of kept_mask. */
 uint32_t pss_mask_words(uint32_t vocab);

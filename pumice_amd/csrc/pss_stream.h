@@ -36,29 +36,30 @@
 #include "pss_general.h"
 
 #define PSS_ST_NT 256
-#define PSS_TOPM_MAX 4u          /* per-lane top-m kept for the bound: K <= 1024 */
-#define PSS_SEG_MAX_N 64u        /* segments per row (V <= 262144 at SEG >= 4096) */
-#define PSS_POOL_CAP 16384u      /* pool entries per row, split evenly over segments */
+#define PSS_SEG_NW 16            /* waves per segment workgroup: one item each per round */
+#define PSS_SEG_NT (PSS_SEG_NW * PSS_WAVE)
+#define PSS_ROW_LIST_CAP 2048u   /* fused form: candidates a workgroup gathers in LDS */
+#define PSS_ROW_BITS 8192u       /* fused form: penalty-bitmap words of the general algorithm */
+#define PSS_SEG_KMAX 256u        /* largest top-k the segment kernel covers (running top-4 per lane) */
+#define PSS_SEG_WMAX 256u        /* largest window the segment kernel covers (four ids per lane) */
+#define PSS_SEG_MAX_SLOTS 256u   /* items per row (V <= 262144 at items >= 1024 ids) */
+#define PSS_POOL_CAP 16384u      /* pool entries per row, split evenly over its items */
 #define PSS_FIN_LIST_CAP 4096u   /* candidates the finisher gathers in LDS */
 #define PSS_FAST_N 1024u         /* candidates the fast finisher handles (K <= 64) */
-#define PSS_SEG_WAVES 4u         /* waves per segment workgroup (PSS_ST_NT / 64) */
 #define PSS_SEG_OVERFLOW 0xFFFFFFFFu
 #define PSS_KEY_NEG_INF 0x007FFFFFu /* pss_key(-inf): the smallest key of any element */
 
 /* Per-row workspace: header, then the candidate pool. */
 struct pss_row_ws {
-    uint32_t bound; /* row-wide lower bound on the K-th largest key (max over segments) */
+    uint32_t bound; /* row-wide lower bound on the K-th largest key (max over items) */
     uint32_t pad[15];
-    uint32_t seg_count[PSS_SEG_MAX_N * PSS_SEG_WAVES]; /* candidates per (segment, wave), or PSS_SEG_OVERFLOW */
-    unsigned long long seg_best[PSS_SEG_MAX_N];  /* greedy rows: (key << 32) | ~id per segment */
+    uint32_t seg_count[PSS_SEG_MAX_SLOTS];          /* candidates per item, or PSS_SEG_OVERFLOW */
+    unsigned long long seg_best[PSS_SEG_MAX_SLOTS]; /* greedy rows: (key << 32) | ~id per item */
 };
 static_assert(sizeof(pss_row_ws) % 64 == 0, "workspace header is a multiple of 64 bytes");
 #define PSS_WS_ROW_BYTES (sizeof(pss_row_ws) + (size_t)PSS_POOL_CAP * 8u)
 
 static inline size_t pss_stream_ws_bytes(uint32_t rows) { return (size_t)rows * PSS_WS_ROW_BYTES; }
-
-/* Pool slots of one (segment, wave) when a row has S segments. */
-__host__ __device__ inline uint32_t pss_wave_cap(uint32_t S) { return PSS_POOL_CAP / (S * PSS_SEG_WAVES); }
 
 __device__ __forceinline__ uint32_t pss_ld_agent(const uint32_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -68,16 +69,29 @@ __device__ __forceinline__ uint32_t pss_ld_agent(const uint32_t* p) {
 /* finisher: selection over the row's candidate list in LDS                  */
 /* ------------------------------------------------------------------------ */
 
-struct pss_fin_shared {
-    unsigned long long list[PSS_FIN_LIST_CAP]; /* gathered candidates (key << 32 | id) */
-    unsigned long long kept[64];               /* fast path: entries >= the K-th largest */
-    uint32_t hist[256];                        /* fast path: radix digit counts */
+/* Fused form: the workgroup's candidate list and row-level values. */
+struct pss_row_lds {
+    unsigned long long list[PSS_ROW_LIST_CAP]; /* (key << 32) | id */
+    unsigned long long best;                   /* greedy rows: (key << 32) | ~id */
+    uint32_t n;                                /* entries claimed (may exceed the capacity) */
+    uint32_t bound;                            /* largest certified bound of the row */
+};
+
+/* Finisher scratch besides the candidate list. */
+struct pss_fin_small {
+    unsigned long long kept[64]; /* fast path: entries >= the K-th largest */
+    uint32_t hist[256];          /* fast path: radix digit counts */
     pss_gen_shared g;
-    uint32_t mx[PSS_ST_NT / PSS_WAVE];         /* per-wave largest key */
+    uint32_t mx[PSS_SEG_NW];     /* per-wave largest key */
     uint32_t digit;
     uint32_t rem;
     uint32_t nk;
     uint32_t fail;
+};
+
+struct pss_fin_shared {
+    unsigned long long list[PSS_FIN_LIST_CAP]; /* gathered candidates (key << 32 | id) */
+    pss_fin_small f;
 };
 
 /*
@@ -239,7 +253,7 @@ struct pss_row_pre {
 };
 
 /*
- * Fast finisher for K <= 64 and up to PSS_FAST_N candidates (sh.list), those
+ * Fast finisher for K <= 64 and up to PSS_FAST_N candidates (list), those
  * below the row-wide bound G ignored:
  *   1. the row's K-th largest by an LDS radix select (8-bit digits), starting
  *      at the first digit below the common prefix of G and the row maximum --
@@ -253,10 +267,11 @@ struct pss_row_pre {
  */
 template <int NT>
 __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t row,
-                                                     const pss_rowcfg& c, uint32_t n, uint32_t G,
-                                                     const pss_row_pre& pre, pss_fin_shared& sh) {
+                                                     const pss_rowcfg& c, const unsigned long long* list,
+                                                     uint32_t n, uint32_t G, const pss_row_pre& pre,
+                                                     pss_fin_small& sh) {
     constexpr int R = (int)(PSS_FAST_N / NT);
-    static_assert(NT == 256, "one radix bin per thread");
+    static_assert(NT >= 256 && NT <= 1024 && PSS_FAST_N % NT == 0, "radix bins: the first 256 threads");
     if (c.K > 64u || n > PSS_FAST_N) return false;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     uint64_t e[R];
@@ -265,7 +280,7 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t i = tid + (uint32_t)r * NT;
-        e[r] = i < n ? sh.list[i] : 0ull;
+        e[r] = i < n ? list[i] : 0ull;
         k[r] = (uint32_t)(e[r] >> 32);
         if (k[r] < G) k[r] = 0u;
         kmax = k[r] > kmax ? k[r] : kmax;
@@ -288,7 +303,7 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
         uint32_t prefix = tmaxKey & pmask;
         uint32_t rem = c.K;
         for (; shift >= 0; shift -= 8) {
-            sh.hist[tid] = 0u;
+            if (tid < 256u) sh.hist[tid] = 0u;
             __syncthreads();
 #pragma unroll
             for (int r = 0; r < R; ++r)
@@ -405,87 +420,73 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
 }
 
 /* ------------------------------------------------------------------------ */
-/* segment kernel                                                            */
+/* segment kernel: independent persistent waves                              */
 /* ------------------------------------------------------------------------ */
 
 template <int EPT, int DT>
-struct pss_seg_geom {
+struct pss_wgeom {
     static constexpr int E = (DT == PSS_DTYPE_F16) ? 8 : 4; /* elements per 16-byte load */
     static constexpr int NL = EPT / E;                      /* loads per lane */
-    static constexpr uint32_t SEG = (uint32_t)PSS_ST_NT * EPT;
-    static constexpr int HPT = (int)((PSS_MAX_PENALTY_LEN + PSS_ST_NT - 1) / PSS_ST_NT);
+    static constexpr uint32_t ITEM = (uint32_t)PSS_WAVE * EPT; /* ids per item */
+    static constexpr int HPT = 4;                            /* window ids per lane held in registers */
     static_assert(EPT % E == 0, "EPT must be a multiple of the load width");
+    static_assert(EPT <= 32, "one claim bit per register index in a 32-bit word");
 };
 
-/* LDS of a segment workgroup.  The penalty bitmap is transposed: word w is
- * thread w's, bit i its register t[i]; it and the per-wave bound exchange
- * are double-buffered (alternating per item that uses them) and cleared by
- * their readers, so an item needs no barrier before it writes them. */
-struct pss_seg_shared {
-    uint32_t pen[2][PSS_ST_NT];          /* window-id bits per thread */
-    uint32_t penOr[2][PSS_SEG_WAVES];    /* OR of the words of each wave */
-    uint32_t lb[2][PSS_SEG_WAVES];       /* per-wave bounds (K <= 256) */
-    uint32_t topm[PSS_ST_NT * PSS_TOPM_MAX];
-    uint64_t red[PSS_ST_NT / PSS_WAVE];
+/* LDS of one wave: the staging area of its item (lane l's 16-byte load li at
+ * stage[li][l], the layout of a wave's load-to-LDS) and the claim bits of
+ * window ids (word l = lane l, bit i = its register t[i]). */
+template <int EPT, int DT>
+struct pss_wave_lds {
+    uint4 stage[pss_wgeom<EPT, DT>::NL][PSS_WAVE];
+    uint32_t claim[PSS_WAVE];
 };
-
-/* Lower bound of one segment's K-th largest: the K-th largest of the lanes'
- * top-m keys to 16 bits (R = 4m values per lane of a wave; every wave
- * computes the same value). */
-template <int R>
-__device__ __forceinline__ uint32_t pss_lane_bound(const uint32_t* topm, uint32_t K) {
-    uint32_t v[R];
-    const uint32_t lane = pss_tid() & 63u;
-#pragma unroll
-    for (int i = 0; i < R; ++i) v[i] = topm[lane * R + i];
-    return wave_kth_largest_r4<R>(v, K, 0u, 31, 16);
-}
 
 /* Row tests from the raw parameters (no division).  A row is covered when
- * it is greedy or its top-k is on and at most 1024 (otherwise the finisher
- * runs the general algorithm on it and the segment kernel skips it). */
+ * it is greedy, or its top-k is on and at most PSS_SEG_KMAX and its window
+ * at most PSS_SEG_WMAX ids; the finisher runs the general algorithm on the
+ * others and the segment kernel skips them. */
 __device__ __forceinline__ bool pss_seg_row_greedy(const pss_args& a, const sample_params& sp) {
     return (a.mode == PSS_MODE_GREEDY) || !(sp.temperature > 0.0f);
 }
 __device__ __forceinline__ bool pss_seg_row_covered(const pss_args& a, const sample_params& sp) {
     const uint32_t K = sp.topK < a.V ? sp.topK : a.V;
-    return pss_seg_row_greedy(a, sp) || (K > 0u && K <= (uint32_t)PSS_ST_NT * PSS_TOPM_MAX);
+    return pss_seg_row_greedy(a, sp) || (K > 0u && K <= PSS_SEG_KMAX && sp.penaltyLength <= PSS_SEG_WMAX);
 }
 
 /* Buffer resource word 3 for raw (untyped, stride 0) buffer loads on gfx9
  * CDNA parts: 32-bit data format, no swizzle, no index stride. */
 #define PSS_BUF_DW3 0x00020000
 
-/* Issue the loads of segment `seg` of `row` into raw[]; nothing here waits
- * for them.  Raw buffer loads over the row (num_records = V * element size):
- * the hardware returns 0 for ids at or beyond V, which the compute step
- * replaces by -inf.  vec_ok (16-byte aligned rows, V a multiple of the
- * elements per 16 bytes): one 16-byte load per 4 fp32 / 8 fp16; otherwise one
- * load per element. */
-template <int EPT, int DT>
-__device__ __forceinline__ void pss_seg_issue(const pss_args& a, uint32_t row, uint32_t seg,
-                                              uint4 (&raw)[pss_seg_geom<EPT, DT>::NL]) {
-    using Gm = pss_seg_geom<EPT, DT>;
-    constexpr int E = Gm::E, NL = Gm::NL;
-    constexpr uint32_t NT = PSS_ST_NT;
-    constexpr uint32_t esz = DT == PSS_DTYPE_F16 ? 2u : 4u;
-    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t pss_row_rsrc(const pss_args& a, uint32_t row, uint32_t esz) {
     const char* rowp = (const char*)a.logits + (size_t)row * a.stride * esz;
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)rowp, (short)0, (int)(a.V * esz), PSS_BUF_DW3);
-    const uint32_t tid = pss_tid();
-    const uint32_t base = seg * Gm::SEG;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)rowp, (short)0, (int)(a.V * esz), PSS_BUF_DW3);
+}
+
+/* Item s of a row into the wave's staging area.  vec_ok (16-byte aligned
+ * rows, V * element size a multiple of 16): raw buffer loads straight to LDS,
+ * nothing waited for and no registers held; the hardware returns 0 for ids
+ * at or beyond V.  Otherwise one buffer load per element into registers,
+ * waited for, then copied to the staging area. */
+template <int EPT, int DT>
+__device__ __forceinline__ void pss_wave_issue(const pss_args& a, uint32_t row, uint32_t s,
+                                               pss_wave_lds<EPT, DT>& wl) {
+    using Gm = pss_wgeom<EPT, DT>;
+    constexpr int E = Gm::E, NL = Gm::NL;
+    constexpr uint32_t esz = DT == PSS_DTYPE_F16 ? 2u : 4u;
+    const __amdgpu_buffer_rsrc_t rs = pss_row_rsrc(a, row, esz);
+    const uint32_t lane = pss_tid() & 63u;
+    const uint32_t base = s * Gm::ITEM;
     if (a.vec_ok) {
 #pragma unroll
-        for (int li = 0; li < NL; ++li) {
-            const v4u v = __builtin_amdgcn_raw_buffer_load_b128(
-                rs, (int)((base + (uint32_t)li * (NT * E) + tid * E) * esz), 0, 0);
-            raw[li] = make_uint4(v.x, v.y, v.z, v.w);
-        }
+        for (int li = 0; li < NL; ++li)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void*)&wl.stage[li][0], 16, (int)(lane * 16u),
+                (int)((base + (uint32_t)li * (PSS_WAVE * E)) * esz), 0, 0);
     } else {
 #pragma unroll
         for (int li = 0; li < NL; ++li) {
-            const uint32_t j0 = base + (uint32_t)li * (NT * E) + tid * E;
+            const uint32_t j0 = base + (uint32_t)li * (PSS_WAVE * E) + lane * E;
             uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
             for (int e = 0; e < E; ++e) {
@@ -495,32 +496,31 @@ __device__ __forceinline__ void pss_seg_issue(const pss_args& a, uint32_t row, u
                 else
                     w[e] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)((j0 + e) * 4u), 0, 0);
             }
-            raw[li] = make_uint4(w[0], w[1], w[2], w[3]);
+            wl.stage[li][lane] = make_uint4(w[0], w[1], w[2], w[3]);
         }
     }
 }
 
-/* Per-item values loaded ahead of the item: the row's window ids (sampled
- * rows with a penalty) and the row-wide bound published so far. */
-template <int HPT>
-struct pss_seg_side {
-    uint32_t hid[HPT];
+/* Per-item values loaded ahead of the item: the row's window ids (at most
+ * PSS_SEG_WMAX on covered rows; sampled rows with a window, the compute step
+ * decides exactly whether a penalty applies) and the row-wide bound
+ * published so far. */
+struct pss_wave_side {
+    uint32_t hid[4];
     uint32_t G0;
 };
 
-template <int HPT>
-__device__ __forceinline__ void pss_seg_side_load(const pss_args& a, uint32_t row, const sample_params& sp,
-                                                  pss_seg_side<HPT>& sd) {
-    /* the window ids of sampled rows with a window (a superset of the rows
-     * that apply a penalty; the compute step decides exactly) */
+__device__ __forceinline__ void pss_wave_side_load(const pss_args& a, uint32_t row, const sample_params& sp,
+                                                   pss_wave_side& sd, bool with_bound) {
     const bool greedy = pss_seg_row_greedy(a, sp);
     const uint32_t W = sp.penaltyLength < PSS_MAX_PENALTY_LEN ? sp.penaltyLength : PSS_MAX_PENALTY_LEN;
     const uint32_t* hist_row = a.history + (size_t)row * PSS_MAX_PENALTY_LEN;
+    const uint32_t lane = pss_tid() & 63u;
 #pragma unroll
-    for (int h = 0; h < HPT; ++h) {
-        const uint32_t idx = pss_tid() + (uint32_t)h * PSS_ST_NT;
+    for (int h = 0; h < 4; ++h) {
+        const uint32_t idx = lane + (uint32_t)h * PSS_WAVE;
         sd.hid[h] = PSS_SENTINEL;
-        if (!greedy && idx < W) sd.hid[h] = hist_row[idx];
+        if (!greedy && W > (uint32_t)h * PSS_WAVE && idx < W) sd.hid[h] = hist_row[idx];
     }
     const pss_row_ws* ws = (const pss_row_ws*)((const char*)a.ws + (size_t)row * PSS_WS_ROW_BYTES);
     /* The lane-varying (zero) offset keeps the value in a vector register:
@@ -528,7 +528,24 @@ __device__ __forceinline__ void pss_seg_side_load(const pss_args& a, uint32_t ro
      * waits for every load issued before it. */
     uint32_t z = 0u;
     __asm__ __volatile__("" : "+v"(z));
-    sd.G0 = greedy ? 0u : pss_ld_agent(&ws->bound + z);
+    sd.G0 = (greedy || !with_bound) ? 0u : pss_ld_agent(&ws->bound + z);
+}
+
+/* The K-th largest (1 <= K <= 64 R) of the R keys of each of the 64 lanes,
+ * to 16 bits: the largest x with at least K keys >= x, one bit per round
+ * (ballots; every lane gets the same value). */
+template <int R>
+__device__ __forceinline__ uint32_t pss_wave_kth16(const uint32_t (&v)[R], uint32_t K) {
+    uint32_t x = 0u;
+#pragma unroll
+    for (int bit = 31; bit >= 16; --bit) {
+        const uint32_t y = x | (1u << bit);
+        uint32_t n = 0u;
+#pragma unroll
+        for (int r = 0; r < R; ++r) n += (uint32_t)__popcll(__ballot(v[r] >= y));
+        x = n >= K ? y : x;
+    }
+    return x;
 }
 
 /* t[i] for a lane-varying index i (a select tree over the bits of i). */
@@ -547,342 +564,409 @@ __device__ __forceinline__ float pss_pick(const float (&t)[N], uint32_t i) {
     return cur[0];
 }
 
-/*
- * One segment (seg, row) whose loads are in raw[].  `carry` is the largest
- * bound this workgroup has established for `carry_row`: every bound is a lower
- * bound of the row's K-th largest, so later segments of the row reuse it
- * instead of deriving their own.
- */
-template <int EPT, int DT, bool M1>
-__device__ __forceinline__ void pss_seg_compute(const pss_args& a, pss_seg_shared& sh, uint32_t row, uint32_t seg,
-                                                uint32_t S, const sample_params& sp,
-                                                const uint4 (&raw)[pss_seg_geom<EPT, DT>::NL],
-                                                const pss_seg_side<pss_seg_geom<EPT, DT>::HPT>& sd,
-                                                uint32_t& carry_row, uint32_t& carry, uint32_t& npen,
-                                                uint32_t& nbound) {
-    using Gm = pss_seg_geom<EPT, DT>;
-    constexpr int NT = PSS_ST_NT;
-    constexpr int E = Gm::E, NL = Gm::NL, HPT = Gm::HPT;
-    constexpr uint32_t SEG = Gm::SEG;
-    static_assert(EPT <= 32, "one bit per register index in a 32-bit word");
-    const uint32_t tid = pss_tid();
-    const uint32_t V = a.V;
-    const uint32_t seg_base = seg * SEG;
-    const bool greedy = pss_seg_row_greedy(a, sp);
-    const pss_rowcfg c = pss_make_rowcfg(sp, V);
-    pss_row_ws* ws = (pss_row_ws*)((char*)a.ws + (size_t)row * PSS_WS_ROW_BYTES);
-    const bool doPen = !greedy && c.doPen;
-
-    /* t = l * (1/T) (greedy rows: the raw logit) */
-    const float invT = greedy ? 1.0f : c.invT;
-    const float NEG_INF = pss_u2f(0xFF800000u);
-    float t[EPT];
-#pragma unroll
-    for (int li = 0; li < NL; ++li) {
-        float v[E];
-        if (DT == PSS_DTYPE_F16) {
-            const uint32_t w[4] = {raw[li].x, raw[li].y, raw[li].z, raw[li].w};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint16_t h = (uint16_t)(w[e >> 1] >> ((e & 1) * 16));
-                _Float16 hf;
-                __builtin_memcpy(&hf, &h, 2);
-                v[e] = (float)hf;
-            }
-        } else {
-            v[0] = __uint_as_float(raw[li].x);
-            v[1] = __uint_as_float(raw[li].y);
-            v[2] = __uint_as_float(raw[li].z);
-            v[3] = __uint_as_float(raw[li].w);
-        }
-#pragma unroll
-        for (int e = 0; e < E; ++e) t[li * E + e] = v[e] * invT;
-    }
-
-    /* Penalty: every thread holding a window id of this segment sets the
-     * owner's bit (element offset o lives in thread (o % (256 E)) / E, register
-     * (o / (256 E)) E + o % E) and the owner wave's summary bit; after one
-     * barrier each thread reads and clears its word, and the wave penalizes
-     * only the register indices some of its lanes hold. */
-    if (doPen) {
-        const uint32_t b = npen & 1u;
-        ++npen;
-#pragma unroll
-        for (int h = 0; h < HPT; ++h) {
-            const uint32_t id = sd.hid[h];
-            if (id >= seg_base && id - seg_base < SEG && id < V) {
-                const uint32_t o = id - seg_base;
-                const uint32_t owner = (o % (uint32_t)(NT * E)) / (uint32_t)E;
-                const uint32_t bit = 1u << ((o / (uint32_t)(NT * E)) * (uint32_t)E + o % (uint32_t)E);
-                atomicOr(&sh.pen[b][owner], bit);
-                atomicOr(&sh.penOr[b][owner >> 6], bit);
-            }
-        }
-        __syncthreads();
-        const uint32_t pb = sh.pen[b][tid];
-        const uint32_t wor = __builtin_amdgcn_readfirstlane(sh.penOr[b][tid >> 6]);
-        sh.pen[b][tid] = 0u;
-        if ((tid & 63u) == 0u) sh.penOr[b][tid >> 6] = 0u;
-#pragma unroll
-        for (int i = 0; i < EPT; ++i)
-            if ((wor >> i) & 1u) t[i] = ((pb >> i) & 1u) ? pss_penalize(t[i], c) : t[i];
-    }
-    auto id_of = [&](uint32_t i) -> uint32_t {
-        return seg_base + (i / E) * (NT * E) + tid * E + (i % E);
-    };
-    /* The row's last segment: ids beyond the vocab read 0; they become -inf,
-     * which never passes a bound above key(-inf) and never wins an argmax
-     * tie against a real id (larger id); where every element passes they are
-     * excluded by id. */
-    if (seg_base + SEG > V) {
-#pragma unroll
-        for (int i = 0; i < EPT; ++i) t[i] = id_of((uint32_t)i) < V ? t[i] : NEG_INF;
-    }
-
-    if (greedy) {
-        /* argmax of the canonical value, smallest id on ties */
-        uint64_t best = 0;
-#pragma unroll
-        for (int i = 0; i < EPT; ++i) {
-            const uint64_t b =
-                ((uint64_t)pss_key(pss_canon(t[i])) << 32) | (uint64_t)(0xFFFFFFFFu - id_of((uint32_t)i));
-            if (b > best) best = b;
-        }
-        best = block_max_u64<NT>(best, sh.red);
-        if (tid == 0) ws->seg_best[seg] = best;
-        return;
-    }
-
-    /* Bound (first segment of the row in this workgroup).  max() ignores NaN,
-     * which canonicalizes to -inf; lanes without elements contribute
-     * key(-inf), the smallest key, which never raises the bound above a true
-     * order statistic.
-     *   M1 (K <= 256): every wave sorts its 64 lane maxima; with K' =
-     *   ceil(K / 4), the minimum over the four waves of their K'-th largest
-     *   has at least 4 K' >= K distinct elements of the segment at or above
-     *   it.  Otherwise every lane's sorted top-4 goes to LDS and every wave
-     *   takes the K-th largest of all of them. */
-    uint32_t thr = carry_row == row ? carry : 0u;
-    if (carry_row != row) {
-        uint32_t L;
-        if (M1) {
-            float mx = NEG_INF;
-#pragma unroll
-            for (int i = 0; i < EPT; ++i) mx = fmaxf(mx, t[i]);
-            const uint32_t srt = dpp_sort_asc_u32(pss_key(pss_canon(mx)));
-            const uint32_t kq = (c.K + (uint32_t)PSS_SEG_WAVES - 1u) / (uint32_t)PSS_SEG_WAVES;
-            const uint32_t lw = (uint32_t)__builtin_amdgcn_readlane(srt, (int)(64u - kq));
-            const uint32_t b = nbound & 1u;
-            ++nbound;
-            if ((tid & 63u) == 0u) sh.lb[b][tid >> 6] = lw;
-            __syncthreads();
-            L = min(min(sh.lb[b][0], sh.lb[b][1]), min(sh.lb[b][2], sh.lb[b][3]));
-        } else {
-            const uint32_t m = (c.K + NT - 1u) / NT;
-            uint32_t* topm = sh.topm;
-            /* insertion into a sorted top-4 on floats (NaN mapped to -inf
-             * first; -0 and +0 order arbitrarily but share one canonical key) */
-            float t0 = NEG_INF, t1 = NEG_INF, t2 = NEG_INF, t3 = NEG_INF;
-#pragma unroll
-            for (int i = 0; i < EPT; ++i) {
-                float x = fmaxf(t[i], NEG_INF), y;
-                y = fminf(t0, x);
-                t0 = fmaxf(t0, x);
-                x = y;
-                y = fminf(t1, x);
-                t1 = fmaxf(t1, x);
-                x = y;
-                y = fminf(t2, x);
-                t2 = fmaxf(t2, x);
-                x = y;
-                t3 = fmaxf(t3, x);
-            }
-            __syncthreads(); /* the previous item's reads of topm are done */
-            topm[tid * m + 0] = pss_key(pss_canon(t0));
-            if (m > 1u) topm[tid * m + 1] = pss_key(pss_canon(t1));
-            if (m > 2u) topm[tid * m + 2] = pss_key(pss_canon(t2));
-            if (m > 3u) topm[tid * m + 3] = pss_key(pss_canon(t3));
-            __syncthreads();
-            if (m == 1u)
-                L = pss_lane_bound<4>(topm, c.K);
-            else if (m == 2u)
-                L = pss_lane_bound<8>(topm, c.K);
-            else if (m == 3u)
-                L = pss_lane_bound<12>(topm, c.K);
-            else
-                L = pss_lane_bound<16>(topm, c.K);
-        }
-        thr = L > thr ? L : thr;
-    }
-    const uint32_t G0 = __builtin_amdgcn_readfirstlane(sd.G0);
-    if (tid == 0 && thr > G0 && thr > PSS_KEY_NEG_INF)
-        (void)__hip_atomic_fetch_max(&ws->bound, thr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    thr = G0 > thr ? G0 : thr;
-    carry_row = row;
-    carry = thr;
-
-    /* Candidates (key >= thr), written by each wave to its own slot range
-     * of the pool: a pass mask per lane, a wave scan of the counts, then each
-     * lane stores its entries (one select tree per entry).  Above key(-inf)
-     * the test is a float compare (t >= unkey(thr) is false for NaN, which
-     * canonicalizes to -inf < thr); at or below it every element of the vocab
-     * passes. */
-    /* bit i of pm: element i passes (built from the top bit down as
-     * pm + pm + pass, a shift-in with no per-bit constants) */
-    uint32_t pm = 0;
-    if (thr <= PSS_KEY_NEG_INF) {
-#pragma unroll
-        for (int i = EPT - 1; i >= 0; --i) pm = pm + pm + (id_of((uint32_t)i) < V ? 1u : 0u);
-    } else {
-        const float thr_f = pss_unkey(thr);
-#pragma unroll
-        for (int i = EPT - 1; i >= 0; --i) pm = pm + pm + (t[i] >= thr_f ? 1u : 0u);
-    }
-    const uint32_t mine = (uint32_t)__popc(pm);
-    const uint32_t incl = wave_incl_scan_u32(mine);
-    const uint32_t wtot = wave_read_u32(incl, 63);
-    const uint32_t slot = seg * PSS_SEG_WAVES + (tid >> 6);
-    const uint32_t capw = pss_wave_cap(S);
-    if (wtot <= capw) {
-        unsigned long long* out = (unsigned long long*)(ws + 1) + (size_t)slot * capw + (incl - mine);
-        while (pm) {
-            const uint32_t i = (uint32_t)__builtin_ctz(pm);
-            pm &= pm - 1u;
-            *out++ = ((unsigned long long)pss_key(pss_canon(pss_pick(t, i))) << 32) | id_of(i);
-        }
-    }
-    if ((tid & 63u) == 0u) ws->seg_count[slot] = wtot <= capw ? wtot : PSS_SEG_OVERFLOW;
-}
-
-/* Staging area of one workgroup: each wave's 16-byte loads of one item, lane
- * l of wave w at v[li][w][l] (the layout of a wave's load-to-LDS). */
-template <int EPT, int DT>
-struct pss_seg_stage {
-    uint4 v[pss_seg_geom<EPT, DT>::NL][PSS_SEG_WAVES][PSS_WAVE];
+/* Running state of a wave over the items of one row: the row's constants
+ * and each lane's largest values so far (M1: one; otherwise a sorted top-4). */
+struct pss_wave_run {
+    uint32_t row;
+    pss_rowcfg c;
+    float top[4];
 };
 
-/* Issue item (row, seg)'s 16-byte loads straight into the calling wave's part
- * of the staging area (raw buffer loads to LDS: no registers held while they
- * are in flight; 0 for ids at or beyond V).  Requires vec_ok. */
-template <int EPT, int DT>
-__device__ __forceinline__ void pss_seg_issue_lds(const pss_args& a, uint32_t row, uint32_t seg,
-                                                  pss_seg_stage<EPT, DT>& st) {
-    using Gm = pss_seg_geom<EPT, DT>;
+/*
+ * Persistent segment kernel.  Item i = (row i / NS, item i % NS of the row),
+ * 64 EPT consecutive ids.  Workgroup b (PSS_SEG_NW waves) takes items
+ * [b per_wg, min((b + 1) per_wg, n_items)), normally whole rows, in rounds:
+ * in round r wave w processes item b per_wg + r PSS_SEG_NW + w.  Per round
+ * and wave:
+ *   A  wait for the item's logits (streamed into the wave's staging area
+ *      during the previous round), claim its window ids (a returning LDS or
+ *      on a claim bit makes exactly one lane the owner of each id: it reads
+ *      the raw value, writes -inf in its place and computes the penalized
+ *      value itself), move the item to registers, start the next round's
+ *      loads, t = l * (1/T), update the lanes' running top values of the
+ *      row (distinct elements outside the window), publish (row, the
+ *      ceil(K / NW)-th largest of them) in LDS;
+ *   -  one barrier;
+ *   B  bound: when every wave's slot holds this row, their minimum has at
+ *      least K elements of the row at or above it (otherwise the wave's own
+ *      K-th largest); raised by the row-wide bound of other workgroups and
+ *      published there.  Then the elements at or above it, and the penalized
+ *      window elements at or above it, into the item's slot range of the
+ *      row's pool (a pass mask per lane, a wave scan of the counts, one
+ *      select tree per entry).  Greedy rows store the item's (max key,
+ *      smallest id) instead.
+ * A slot only rises within a row, and a wave reads other slots after the
+ * barrier, so a slot already rewritten in the next round is still a valid
+ * certificate (or a different row, which only withholds the joint bound).
+ * M1: every row of the launch has K <= 64 (one running value per lane);
+ * otherwise a running top-4 per lane (K <= 256).  `params` is a.params as a
+ * restrict argument: the kernel's stores cannot alias it, so the row
+ * parameters of later items still come through scalar loads.
+ */
+template <int EPT, int DT, bool M1, bool FUSED>
+__device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, uint32_t i0, uint32_t i1,
+                                               const sample_params* __restrict__ params,
+                                               pss_wave_lds<EPT, DT>* lds, unsigned long long* joint,
+                                               pss_row_lds* rl) {
+    using Gm = pss_wgeom<EPT, DT>;
     constexpr int E = Gm::E, NL = Gm::NL;
-    constexpr uint32_t NT = PSS_ST_NT;
+    constexpr uint32_t ITEM = Gm::ITEM;
+    constexpr uint32_t NW = PSS_SEG_NW;
     constexpr uint32_t esz = DT == PSS_DTYPE_F16 ? 2u : 4u;
-    const char* rowp = (const char*)a.logits + (size_t)row * a.stride * esz;
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)rowp, (short)0, (int)(a.V * esz), PSS_BUF_DW3);
-    const uint32_t tid = pss_tid();
-    const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t base = seg * Gm::SEG;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(pss_tid() >> 6);
+    const uint32_t lane = pss_tid() & 63u;
+    pss_wave_lds<EPT, DT>& wl = lds[wave];
+    if (lane == 0u) joint[wave] = ~0ull;
+    wl.claim[lane] = 0u;
+    __syncthreads();
+    const uint32_t V = a.V;
+    const float NEG_INF = pss_u2f(0xFF800000u);
+    const uint32_t R = (i1 - i0 + NW - 1u) / NW;
+
+    pss_wave_run run;
+    run.row = 0xFFFFFFFFu;
+    const pss_wave_side none = {{PSS_SENTINEL, PSS_SENTINEL, PSS_SENTINEL, PSS_SENTINEL}, 0u};
+    pss_wave_side sd = none;
+    uint32_t it = i0 + wave;
+    bool act = it < i1;
+    uint32_t row = act ? it / NS : i0 / NS;
+    uint32_t s = act ? it - row * NS : 0u;
+    sample_params sp = params[row];
+    bool cov = act && pss_seg_row_covered(a, sp);
+    if (cov) {
+        pss_wave_issue<EPT, DT>(a, row, s, wl);
+        pss_wave_side_load(a, row, sp, sd, !FUSED);
+    }
+    for (uint32_t r = 0; r < R; ++r) {
+        const uint32_t nit = it + NW;
+        const bool nact = nit < i1;
+        const uint32_t nrow = nact ? nit / NS : row;
+        const uint32_t ns = nact ? nit - nrow * NS : 0u;
+        const sample_params nsp = params[nrow];
+        const bool ncov = nact && pss_seg_row_covered(a, nsp);
+        pss_wave_side nsd = none;
+
+        /* ---- A ---- */
+        const bool greedy = pss_seg_row_greedy(a, sp);
+        const uint32_t base = s * ITEM;
+        float t[EPT];
+        float ov[4] = {NEG_INF, NEG_INF, NEG_INF, NEG_INF};
+        uint32_t ovid[4] = {0u, 0u, 0u, 0u};
+        uint32_t ovn = 0u; /* bit h: hid[h] is this lane's override */
+        uint32_t pw = 0u;  /* this lane's claimed register indices */
+        float cur = NEG_INF;
+        if (cov) {
+            if (run.row != row) {
+                run.row = row;
+                run.c = pss_make_rowcfg(sp, V);
+                run.top[0] = run.top[1] = run.top[2] = run.top[3] = NEG_INF;
+            }
+            const pss_rowcfg& c = run.c;
+            const bool doPen = !greedy && c.doPen;
+            const float invT = greedy ? 1.0f : c.invT;
+            pss_wait_mem(); /* this item's staged loads and side values */
+            __asm__ __volatile__("" ::: "memory");
+            if (doPen) {
 #pragma unroll
-    for (int li = 0; li < NL; ++li)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rs, (__attribute__((address_space(3))) void*)&st.v[li][w][0], 16,
-            (int)((base + (uint32_t)li * (NT * E) + tid * E) * esz), 0, 0, 0);
+                for (int h = 0; h < 4; ++h) {
+                    const uint32_t id = sd.hid[h];
+                    const bool inr = id >= base && id - base < ITEM && id < V;
+                    if (c.W > (uint32_t)h * PSS_WAVE && __ballot(inr) != 0ull && inr) {
+                        const uint32_t o = id - base;
+                        const uint32_t li = o / (uint32_t)(PSS_WAVE * E), rr = o % (uint32_t)(PSS_WAVE * E);
+                        const uint32_t owner = rr / (uint32_t)E, e = rr % (uint32_t)E;
+                        const uint32_t bit = 1u << (li * (uint32_t)E + e);
+                        const uint32_t old = atomicOr(&wl.claim[owner], bit);
+                        if (!(old & bit)) {
+                            char* p = (char*)&wl.stage[li][owner] + e * esz;
+                            float x;
+                            if (DT == PSS_DTYPE_F16) {
+                                _Float16 hf;
+                                __builtin_memcpy(&hf, p, 2);
+                                x = (float)hf;
+                                const uint16_t ninf = 0xFC00u;
+                                __builtin_memcpy(p, &ninf, 2);
+                            } else {
+                                x = *(float*)p;
+                                *(float*)p = NEG_INF;
+                            }
+                            ov[h] = pss_penalize(x * invT, c);
+                            ovid[h] = id;
+                            ovn |= 1u << h;
+                        }
+                    }
+                }
+            }
+            uint4 raw[NL];
+#pragma unroll
+            for (int li = 0; li < NL; ++li) raw[li] = wl.stage[li][lane];
+            if (doPen) {
+                pw = wl.claim[lane];
+                wl.claim[lane] = 0u;
+            }
+            pss_wait_mem(); /* the staging area is free again */
+            __asm__ __volatile__("" ::: "memory");
+            if (ncov) {
+                pss_wave_issue<EPT, DT>(a, nrow, ns, wl);
+                pss_wave_side_load(a, nrow, nsp, nsd, !FUSED);
+                __asm__ __volatile__("" ::: "memory");
+            }
+#pragma unroll
+            for (int li = 0; li < NL; ++li) {
+                float v[E];
+                if (DT == PSS_DTYPE_F16) {
+                    const uint32_t w[4] = {raw[li].x, raw[li].y, raw[li].z, raw[li].w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const uint16_t h = (uint16_t)(w[e >> 1] >> ((e & 1) * 16));
+                        _Float16 hf;
+                        __builtin_memcpy(&hf, &h, 2);
+                        v[e] = (float)hf;
+                    }
+                } else {
+                    v[0] = __uint_as_float(raw[li].x);
+                    v[1] = __uint_as_float(raw[li].y);
+                    v[2] = __uint_as_float(raw[li].z);
+                    v[3] = __uint_as_float(raw[li].w);
+                }
+#pragma unroll
+                for (int e = 0; e < E; ++e) t[li * E + e] = v[e] * invT;
+            }
+            /* The row's last item: ids beyond the vocab read 0; they become
+             * -inf, which never passes a bound above key(-inf) and never
+             * wins an argmax tie against a real id (larger id); where every
+             * element passes they are excluded by id. */
+            if (base + ITEM > V) {
+#pragma unroll
+                for (int i = 0; i < EPT; ++i)
+                    t[i] = base + (uint32_t)(i / E) * (PSS_WAVE * E) + lane * E + (uint32_t)(i % E) < V ? t[i]
+                                                                                                        : NEG_INF;
+            }
+            if (greedy) {
+                /* argmax of the canonical value, smallest id on ties */
+                uint64_t best = 0;
+#pragma unroll
+                for (int i = 0; i < EPT; ++i) {
+                    const uint32_t id = base + (uint32_t)(i / E) * (PSS_WAVE * E) + lane * E + (uint32_t)(i % E);
+                    const uint64_t b = ((uint64_t)pss_key(pss_canon(t[i])) << 32) | (uint64_t)(0xFFFFFFFFu - id);
+                    best = b > best ? b : best;
+                }
+                best = wave_max_u64(best);
+                if (FUSED) {
+                    if (lane == 0u) atomicMax(&rl->best, (unsigned long long)best);
+                } else {
+                    pss_row_ws* ws = (pss_row_ws*)((char*)a.ws + (size_t)row * PSS_WS_ROW_BYTES);
+                    if (lane == 0u) ws->seg_best[s] = best;
+                }
+            } else {
+                /* running values; fmaxf ignores NaN, which canonicalizes to
+                 * -inf; -inf (window and padding elements, lanes without
+                 * elements) never raises a bound above an order statistic */
+#pragma unroll
+                for (int i = 0; i < EPT; ++i) cur = fmaxf(cur, t[i]);
+                uint32_t T;
+                const uint32_t kq = (c.K + NW - 1u) / NW;
+                if (M1) {
+                    run.top[0] = fmaxf(run.top[0], cur);
+                    const uint32_t k1[1] = {pss_key(pss_canon(run.top[0]))};
+                    T = pss_wave_kth16<1>(k1, kq);
+                } else {
+                    float t0 = run.top[0], t1 = run.top[1], t2 = run.top[2], t3 = run.top[3];
+#pragma unroll
+                    for (int i = 0; i < EPT; ++i) {
+                        float x = fmaxf(t[i], NEG_INF), y;
+                        y = fminf(t0, x);
+                        t0 = fmaxf(t0, x);
+                        x = y;
+                        y = fminf(t1, x);
+                        t1 = fmaxf(t1, x);
+                        x = y;
+                        y = fminf(t2, x);
+                        t2 = fmaxf(t2, x);
+                        x = y;
+                        t3 = fmaxf(t3, x);
+                    }
+                    run.top[0] = t0, run.top[1] = t1, run.top[2] = t2, run.top[3] = t3;
+                    const uint32_t k4[4] = {pss_key(pss_canon(t0)), pss_key(pss_canon(t1)), pss_key(pss_canon(t2)),
+                                            pss_key(pss_canon(t3))};
+                    T = pss_wave_kth16<4>(k4, kq);
+                }
+                if (lane == 0u) joint[wave] = ((unsigned long long)row << 32) | T;
+            }
+        } else if (ncov) {
+            pss_wave_issue<EPT, DT>(a, nrow, ns, wl);
+            pss_wave_side_load(a, nrow, nsp, nsd, !FUSED);
+        }
+        __syncthreads();
+
+        /* ---- B ---- */
+        if (cov && !greedy) {
+            const pss_rowcfg& c = run.c;
+            pss_row_ws* ws = (pss_row_ws*)((char*)a.ws + (size_t)row * PSS_WS_ROW_BYTES);
+            /* joint certificate: all NW slots on this row */
+            const unsigned long long e = joint[lane % NW];
+            const bool bad = (uint32_t)(e >> 32) != row;
+            uint32_t L = 0u;
+            if (__ballot(bad) == 0ull) {
+                L = (uint32_t)e;
+                L = min(L, lane_xor<1>(L));
+                L = min(L, lane_xor<2>(L));
+                L = min(L, lane_xor<4>(L));
+                L = min(L, lane_xor<8>(L));
+                L = __builtin_amdgcn_readfirstlane(L);
+            } else if (M1) {
+                const uint32_t k1[1] = {pss_key(pss_canon(run.top[0]))};
+                L = pss_wave_kth16<1>(k1, c.K);
+            } else {
+                const uint32_t k4[4] = {pss_key(pss_canon(run.top[0])), pss_key(pss_canon(run.top[1])),
+                                        pss_key(pss_canon(run.top[2])), pss_key(pss_canon(run.top[3]))};
+                L = pss_wave_kth16<4>(k4, c.K);
+            }
+            uint32_t thr = L;
+            if (FUSED) {
+                if (lane == 0u && L > PSS_KEY_NEG_INF) atomicMax(&rl->bound, L);
+            } else {
+                const uint32_t G0 = __builtin_amdgcn_readfirstlane(sd.G0);
+                if (lane == 0u && L > G0 && L > PSS_KEY_NEG_INF)
+                    (void)__hip_atomic_fetch_max(&ws->bound, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                thr = L > G0 ? L : G0;
+            }
+
+            /* candidates (key >= thr) into the item's slot range.  Above
+             * key(-inf) the test is a float compare (false for NaN, which
+             * canonicalizes to -inf < thr); at or below it every element of
+             * the vocab passes (claimed window elements through their
+             * overrides).  A wave with no candidate skips the mask. */
+            auto id_of = [&](uint32_t i) -> uint32_t {
+                return base + (i / E) * (PSS_WAVE * E) + lane * E + (i % E);
+            };
+            const uint32_t capw = FUSED ? PSS_ROW_LIST_CAP : PSS_POOL_CAP / NS;
+            uint32_t pm = 0u, ovp = 0u;
+            bool any = true;
+            if (thr <= PSS_KEY_NEG_INF) {
+#pragma unroll
+                for (int i = EPT - 1; i >= 0; --i) pm = pm + pm + (id_of((uint32_t)i) < V ? 1u : 0u);
+                pm &= ~pw;
+                ovp = ovn;
+            } else {
+                const float thr_f = pss_unkey(thr);
+#pragma unroll
+                for (int h = 0; h < 4; ++h) ovp |= (((ovn >> h) & 1u) && ov[h] >= thr_f) ? 1u << h : 0u;
+                any = __ballot(cur >= thr_f || ovp != 0u) != 0ull;
+                if (any) {
+#pragma unroll
+                    for (int i = EPT - 1; i >= 0; --i) pm = pm + pm + (t[i] >= thr_f ? 1u : 0u);
+                }
+            }
+            uint32_t tot = 0u;
+            if (any) {
+                const uint32_t mine = (uint32_t)__popc(pm) + (uint32_t)__popc(ovp);
+                const uint32_t incl = wave_incl_scan_u32(mine);
+                tot = wave_read_u32(incl, 63);
+                /* fused: the wave's range of the workgroup's LDS list */
+                uint32_t lbase = 0u;
+                if (FUSED) {
+                    uint32_t b0 = 0u;
+                    if (lane == 0u && tot) b0 = atomicAdd(&rl->n, tot);
+                    lbase = __builtin_amdgcn_readfirstlane(b0);
+                }
+                if ((FUSED ? lbase + tot <= capw : tot <= capw) && mine) {
+                    unsigned long long* out = FUSED ? rl->list + lbase + (incl - mine)
+                                                    : (unsigned long long*)(ws + 1) + (size_t)s * capw + (incl - mine);
+#pragma unroll
+                    for (int h = 0; h < 4; ++h)
+                        if ((ovp >> h) & 1u) *out++ = ((unsigned long long)pss_key(pss_canon(ov[h])) << 32) | ovid[h];
+                    while (pm) {
+                        const uint32_t i = (uint32_t)__builtin_ctz(pm);
+                        pm &= pm - 1u;
+                        *out++ = ((unsigned long long)pss_key(pss_canon(pss_pick(t, i))) << 32) | id_of(i);
+                    }
+                }
+            }
+            if (!FUSED && lane == 0u) ws->seg_count[s] = tot <= capw ? tot : PSS_SEG_OVERFLOW;
+        }
+        it = nit;
+        row = nrow;
+        s = ns;
+        sp = nsp;
+        cov = ncov;
+        sd = nsd;
+    }
 }
 
-/*
- * Persistent segment kernel: item i = (row i / S, segment i % S); workgroup b
- * processes items [b * per_wg, min((b + 1) * per_wg, n_items)) in order, and
- * the grid is sized to the resident capacity, so every workgroup runs from
- * the start.  Pipeline (vec_ok): while item j is computed from registers, item
- * j + 1's logits stream into the wave's staging area in LDS and its window
- * ids, row-wide bound and parameters are loaded; at the top of the next
- * iteration the wave waits for them and moves its staged loads to registers.
- * Each wave reads back only what its own loads wrote, so the staging area
- * needs no barrier.  Without vec_ok (unaligned rows, V not a multiple of the
- * elements per 16 bytes) every item loads element-wise at its own start.  M1:
- * every row of the launch has K <= 256 (one top value per lane); the general
- * form keeps a sorted top-4 per lane, which costs registers.  `params` is
- * a.params as a restrict argument: the workgroup's stores cannot alias it, so
- * the row parameters of later items still come through scalar loads.
- */
+
+/* Split form: workgroup b takes items [b per_wg, ...) of the launch; the
+ * finisher kernel completes the rows from the workspace pools. */
 template <int EPT, int DT, bool M1>
-__global__ void __launch_bounds__(PSS_ST_NT) pss_seg_kernel(pss_args a, uint32_t S, uint32_t n_items,
-                                                            uint32_t per_wg,
-                                                            const sample_params* __restrict__ params) {
-    using Gm = pss_seg_geom<EPT, DT>;
-    __shared__ pss_seg_shared sh;
-    __shared__ pss_seg_stage<EPT, DT> stage;
+__global__ void __launch_bounds__(PSS_SEG_NT) pss_seg_kernel(pss_args a, uint32_t NS, uint32_t n_items,
+                                                             uint32_t per_wg,
+                                                             const sample_params* __restrict__ params) {
+    __shared__ pss_wave_lds<EPT, DT> lds[PSS_SEG_NW];
+    __shared__ unsigned long long joint[PSS_SEG_NW]; /* (row << 32) | per-wave certificate */
     pss_globalize(a);
     const uint32_t i0 = blockIdx.x * per_wg;
     const uint32_t i1 = i0 + per_wg < n_items ? i0 + per_wg : n_items;
     if (i0 >= i1) return;
-    uint32_t n = i1 - i0; /* items left, the current one included */
-    const bool staged = a.vec_ok != 0u;
+    pss_seg_rounds<EPT, DT, M1, false>(a, NS, i0, i1, params, lds, joint, nullptr);
+}
 
-    uint4 raw[Gm::NL];
-    pss_seg_side<Gm::HPT> sd;
-    uint32_t carry_row = 0xFFFFFFFFu, carry = 0u, npen = 0u, nbound = 0u;
-    auto covered = [&](const sample_params& sp) -> bool { return pss_seg_row_covered(a, sp); };
-    {
-        const uint32_t tid = pss_tid();
-        sh.pen[0][tid] = 0u;
-        sh.pen[1][tid] = 0u;
-        if (tid < 2u * PSS_SEG_WAVES) (&sh.penOr[0][0])[tid] = 0u;
-        __syncthreads();
-    }
+/*
+ * Fused form: workgroup r takes row r whole, gathers its candidates in an LDS
+ * list and finishes the row itself after the last round (no workspace, no
+ * second kernel).  The finisher's scratch shares the staging area, free by
+ * then.  Rows the list cannot finish (top-k off or above PSS_SEG_KMAX, a
+ * window above PSS_SEG_WMAX, more candidates than the list holds) run the
+ * general algorithm in the same workgroup.
+ */
+template <int EPT, int DT>
+union pss_row_scratch {
+    pss_wave_lds<EPT, DT> st[PSS_SEG_NW];
+    struct {
+        pss_fin_small f;
+        uint32_t bits[PSS_ROW_BITS];
+    } fin;
+};
 
-    /* (row, seg) and parameters of the current item and the next two */
-    auto advance = [&](uint32_t& r, uint32_t& g) {
-        if (++g == S) {
-            g = 0u;
-            ++r;
-        }
-    };
-    uint32_t row0 = __builtin_amdgcn_readfirstlane(i0 / S);
-    uint32_t seg0 = i0 - row0 * S;
-    uint32_t row1 = row0, seg1 = seg0;
-    advance(row1, seg1);
-    uint32_t row2 = row1, seg2 = seg1;
-    advance(row2, seg2);
-    sample_params sp0 = params[row0];
-    sample_params sp1 = params[n > 1u ? row1 : row0];
-    if (staged) {
-        pss_seg_issue_lds<EPT, DT>(a, row0, seg0, stage);
-        if (covered(sp0)) pss_seg_side_load<Gm::HPT>(a, row0, sp0, sd);
+template <int EPT, int DT, bool M1>
+__global__ void __launch_bounds__(PSS_SEG_NT) pss_row_kernel(pss_args a, uint32_t NS,
+                                                             const sample_params* __restrict__ params) {
+    constexpr int NT = PSS_SEG_NT;
+    __shared__ pss_row_scratch<EPT, DT> U;
+    __shared__ unsigned long long joint[PSS_SEG_NW];
+    __shared__ pss_row_lds rl;
+    pss_globalize(a);
+    const uint32_t row = blockIdx.x, tid = pss_tid();
+    const sample_params sp = params[row];
+    pss_row_pre pre;
+    pre.rng = a.rng[row];
+    pre.step = a.step[row];
+    pre.pos = a.position[row];
+    if (tid == 0u) {
+        rl.n = 0u;
+        rl.bound = 0u;
+        rl.best = 0ull;
     }
-    for (;;) {
-        const bool more = n > 1u;
-        if (staged) {
-            pss_wait_mem(); /* this item's staged loads and side values */
-            __asm__ __volatile__("" ::: "memory");
-            const uint32_t tid = pss_tid();
-            const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
-#pragma unroll
-            for (int li = 0; li < Gm::NL; ++li) raw[li] = stage.v[li][w][tid & 63u];
-            pss_wait_mem(); /* the staging area is free again */
-            __asm__ __volatile__("" ::: "memory");
-        } else {
-            pss_seg_issue<EPT, DT>(a, row0, seg0, raw);
-            if (covered(sp0)) pss_seg_side_load<Gm::HPT>(a, row0, sp0, sd);
-        }
-        const pss_seg_side<Gm::HPT> cur = sd;
-        const sample_params sp2 = params[n > 2u ? row2 : row0];
-        if (staged && more) {
-            pss_seg_issue_lds<EPT, DT>(a, row1, seg1, stage);
-            if (covered(sp1)) pss_seg_side_load<Gm::HPT>(a, row1, sp1, sd);
-            __asm__ __volatile__("" ::: "memory");
-        }
-        if (covered(sp0))
-            pss_seg_compute<EPT, DT, M1>(a, sh, row0, seg0, S, sp0, raw, cur, carry_row, carry, npen, nbound);
-        if (!more) break;
-        --n;
-        row0 = row1, seg0 = seg1, sp0 = sp1;
-        row1 = row2, seg1 = seg2, sp1 = sp2;
-        advance(row2, seg2);
+    const bool covered = pss_seg_row_covered(a, sp);
+    if (covered) pss_seg_rounds<EPT, DT, M1, true>(a, NS, row * NS, row * NS + NS, params, U.st, joint, &rl);
+    __syncthreads();
+    const pss_rowcfg c = pss_make_rowcfg(sp, a.V);
+    if (pss_seg_row_greedy(a, sp)) {
+        pss_greedy_finish<NT>(a, row, rl.best);
+        return;
     }
+    const uint32_t n = rl.n;
+    bool general = !covered || n > PSS_ROW_LIST_CAP;
+    if (!general && !pss_list_finish_fast<NT>(a, row, c, rl.list, n, rl.bound, pre, U.fin.f))
+        pss_list_finish<NT>(a, row, c, rl.list, n, U.fin.f.g);
+    if (general) pss_general_row<NT>(a, row, U.fin.f.g, U.fin.bits, PSS_ROW_BITS);
 }
 
 /* ------------------------------------------------------------------------ */
 /* finisher kernel                                                           */
 /* ------------------------------------------------------------------------ */
 
-/* One workgroup per row; S segments per row were written by pss_seg_kernel. */
-__global__ void __launch_bounds__(PSS_ST_NT) pss_fin_kernel(pss_args a, uint32_t S) {
+/* One workgroup per row; NS items per row were written by pss_seg_kernel. */
+__global__ void __launch_bounds__(PSS_ST_NT) pss_fin_kernel(pss_args a, uint32_t NS) {
     constexpr int NT = PSS_ST_NT;
     __shared__ pss_fin_shared sh;
     __shared__ uint32_t bits[PSS_MAX_VOCAB / 32];
@@ -900,26 +984,25 @@ __global__ void __launch_bounds__(PSS_ST_NT) pss_fin_kernel(pss_args a, uint32_t
 
     if (greedy) {
         uint64_t best = 0;
-        for (uint32_t s = tid; s < S; s += NT) best = ws->seg_best[s] > best ? ws->seg_best[s] : best;
-        best = block_max_u64<NT>(best, sh.g.red);
+        for (uint32_t s = tid; s < NS; s += NT) best = ws->seg_best[s] > best ? ws->seg_best[s] : best;
+        best = block_max_u64<NT>(best, sh.f.g.red);
         pss_greedy_finish<NT>(a, row, best);
         return;
     }
-    bool general = !(c.K > 0u && c.K <= (uint32_t)NT * PSS_TOPM_MAX);
+    bool general = !pss_seg_row_covered(a, sp);
     if (!general) {
         /* Gather: slot counts in one round trip, their prefix sums, then each
          * slot's owner thread copies its entries to the LDS list at its
          * offset (the entries in one more round trip). */
         const uint32_t G = ws->bound;
-        const uint32_t NS = S * PSS_SEG_WAVES;
-        const uint32_t capw = pss_wave_cap(S);
+        const uint32_t capw = PSS_POOL_CAP / NS;
         const uint32_t ns = tid < NS ? ws->seg_count[tid] : 0u;
         const bool over = ns == PSS_SEG_OVERFLOW;
         const uint32_t n0 = over ? 0u : ns;
-        if (tid == 0) sh.fail = 0;
+        if (tid == 0) sh.f.fail = 0;
         uint64_t total64;
-        const uint32_t off = (uint32_t)block_excl_scan_u64<NT>(n0, sh.g.red, &total64);
-        if (over) sh.fail = 1u;
+        const uint32_t off = (uint32_t)block_excl_scan_u64<NT>(n0, sh.f.g.red, &total64);
+        if (over) sh.f.fail = 1u;
         const uint32_t total = (uint32_t)total64;
         if (n0 && total <= PSS_FIN_LIST_CAP) {
             const unsigned long long* src = (const unsigned long long*)(ws + 1) + (size_t)tid * capw;
@@ -933,28 +1016,27 @@ __global__ void __launch_bounds__(PSS_ST_NT) pss_fin_kernel(pss_args a, uint32_t
             }
         }
         __syncthreads();
-        general = sh.fail != 0u || total > PSS_FIN_LIST_CAP;
-        if (!general && !pss_list_finish_fast<NT>(a, row, c, total, G, pre, sh)) {
+        general = sh.f.fail != 0u || total > PSS_FIN_LIST_CAP;
+        if (!general && !pss_list_finish_fast<NT>(a, row, c, sh.list, total, G, pre, sh.f)) {
             /* slow path: candidates below the row-wide bound may remain in the
              * list; they are below the K-th largest and never selected */
-            pss_list_finish<NT>(a, row, c, sh.list, total, sh.g);
+            pss_list_finish<NT>(a, row, c, sh.list, total, sh.f.g);
         }
         if (tid == 0) ws->bound = 0u; /* for the next launch */
     }
-    if (general) pss_general_row<NT>(a, row, sh.g, bits, PSS_MAX_VOCAB / 32);
+    if (general) pss_general_row<NT>(a, row, sh.f.g, bits, PSS_MAX_VOCAB / 32);
 }
 
 /* ---------------------------------------------------------------------- */
 /* host-side launch                                                        */
 /* ---------------------------------------------------------------------- */
 
-/* Elements per lane: 32 (8192-id segments, one pass bit per element in a
- * 32-bit mask), or 16 for vocabularies that would otherwise exceed
- * PSS_SEG_MAX_N segments (none at V <= 262,144) or give fewer than 8 items. */
+/* Elements per lane: 32 (2048-id items); 16 only if a row would otherwise
+ * need more than PSS_SEG_MAX_SLOTS items (none at V <= 262,144). */
 static inline int pss_stream_pick_ept(uint32_t V, uint32_t rows) {
-    const uint64_t S32 = (V + (uint64_t)PSS_ST_NT * 32u - 1u) / ((uint64_t)PSS_ST_NT * 32u);
-    if (S32 > PSS_SEG_MAX_N || (uint64_t)rows * S32 < 8u) return 16;
-    return 32;
+    (void)rows;
+    const uint64_t n32 = (V + (uint64_t)PSS_WAVE * 32u - 1u) / ((uint64_t)PSS_WAVE * 32u);
+    return n32 > PSS_SEG_MAX_SLOTS ? 16 : 32;
 }
 
 /* Workgroups of a segment kernel instantiation resident on the current
@@ -967,7 +1049,7 @@ static inline uint32_t pss_seg_capacity() {
     if (dev < 64 && cache[dev]) return cache[dev];
     int cus = 0, nb = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, pss_seg_kernel<EPT, DT, M1>, PSS_ST_NT, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, pss_seg_kernel<EPT, DT, M1>, PSS_SEG_NT, 0) !=
         hipSuccess)
         return 0;
     const uint32_t cap = (uint32_t)(nb > 0 ? nb : 1) * (uint32_t)(cus > 0 ? cus : 1);
@@ -975,46 +1057,68 @@ static inline uint32_t pss_seg_capacity() {
     return cap;
 }
 
+/* Grid: items split evenly over at most the resident workgroups, at least
+ * one round (PSS_SEG_NW items) per workgroup. */
 template <int EPT, int DT, bool M1>
-static inline hipError_t pss_seg_launch(const pss_args& a, uint32_t S, uint32_t n_items, hipStream_t st) {
+static inline hipError_t pss_seg_launch(const pss_args& a, uint32_t NS, uint32_t n_items, hipStream_t st) {
     uint32_t cap = pss_seg_capacity<EPT, DT, M1>();
-    if (cap == 0) cap = n_items;
-    const uint32_t per_wg = (n_items + cap - 1u) / cap;
+    if (cap == 0) cap = 1;
+    uint32_t per_wg = (n_items + cap - 1u) / cap;
+    if (per_wg < PSS_SEG_NW) per_wg = PSS_SEG_NW;
     const uint32_t grid = (n_items + per_wg - 1u) / per_wg;
-    pss_seg_kernel<EPT, DT, M1><<<dim3(grid), dim3(PSS_ST_NT), 0, st>>>(a, S, n_items, per_wg, a.params);
+    pss_seg_kernel<EPT, DT, M1><<<dim3(grid), dim3(PSS_SEG_NT), 0, st>>>(a, NS, n_items, per_wg, a.params);
     return hipGetLastError();
 }
 
 template <int EPT>
-static inline hipError_t pss_stream_go(const pss_args& a, uint32_t rows, uint32_t max_k, hipStream_t st,
-                                       hipEvent_t split) {
-    const uint32_t seg = (uint32_t)PSS_ST_NT * EPT;
-    const uint32_t S = (a.V + seg - 1u) / seg;
-    if ((uint64_t)rows * S >= (1ull << 31)) return hipErrorInvalidValue;
-    const uint32_t n_items = rows * S;
-    const bool m1 = max_k <= (uint32_t)PSS_ST_NT;
+static inline hipError_t pss_stream_go(const pss_args& a, uint32_t rows, uint32_t max_k, bool split,
+                                       hipStream_t st, hipEvent_t split_ev) {
+    const uint32_t item = (uint32_t)PSS_WAVE * EPT;
+    const uint32_t NS = (a.V + item - 1u) / item;
+    if (NS > PSS_SEG_MAX_SLOTS || (uint64_t)rows * NS >= (1ull << 31)) return hipErrorInvalidValue;
+    const bool m1 = max_k <= (uint32_t)PSS_WAVE;
     hipError_t e;
+    if (!split) {
+        const dim3 grid(rows), block(PSS_SEG_NT);
+        if (a.dtype == PSS_DTYPE_F16) {
+            if (m1)
+                pss_row_kernel<EPT, PSS_DTYPE_F16, true><<<grid, block, 0, st>>>(a, NS, a.params);
+            else
+                pss_row_kernel<EPT, PSS_DTYPE_F16, false><<<grid, block, 0, st>>>(a, NS, a.params);
+        } else {
+            if (m1)
+                pss_row_kernel<EPT, PSS_DTYPE_F32, true><<<grid, block, 0, st>>>(a, NS, a.params);
+            else
+                pss_row_kernel<EPT, PSS_DTYPE_F32, false><<<grid, block, 0, st>>>(a, NS, a.params);
+        }
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (split_ev && (e = hipEventRecord(split_ev, st)) != hipSuccess) return e;
+        return hipSuccess;
+    }
+    const uint32_t n_items = rows * NS;
     if (a.dtype == PSS_DTYPE_F16)
-        e = m1 ? pss_seg_launch<EPT, PSS_DTYPE_F16, true>(a, S, n_items, st)
-               : pss_seg_launch<EPT, PSS_DTYPE_F16, false>(a, S, n_items, st);
+        e = m1 ? pss_seg_launch<EPT, PSS_DTYPE_F16, true>(a, NS, n_items, st)
+               : pss_seg_launch<EPT, PSS_DTYPE_F16, false>(a, NS, n_items, st);
     else
-        e = m1 ? pss_seg_launch<EPT, PSS_DTYPE_F32, true>(a, S, n_items, st)
-               : pss_seg_launch<EPT, PSS_DTYPE_F32, false>(a, S, n_items, st);
+        e = m1 ? pss_seg_launch<EPT, PSS_DTYPE_F32, true>(a, NS, n_items, st)
+               : pss_seg_launch<EPT, PSS_DTYPE_F32, false>(a, NS, n_items, st);
     if (e != hipSuccess) return e;
-    if (split && (e = hipEventRecord(split, st)) != hipSuccess) return e;
-    pss_fin_kernel<<<dim3(rows), dim3(PSS_ST_NT), 0, st>>>(a, S);
+    if (split_ev && (e = hipEventRecord(split_ev, st)) != hipSuccess) return e;
+    pss_fin_kernel<<<dim3(rows), dim3(PSS_ST_NT), 0, st>>>(a, NS);
     return hipGetLastError();
 }
 
-/* max_k: the largest top-k of the launched rows (an upper bound is enough). */
-static inline hipError_t pss_stream_launch(pss_args a, uint32_t rows, uint32_t max_k, hipStream_t st,
-                                           hipEvent_t split) {
+/* max_k: the largest top-k of the launched rows (an upper bound is enough).
+ * split: the two-kernel form (segment kernel + finisher kernel) instead of
+ * the fused one; both compute the same bits. */
+static inline hipError_t pss_stream_launch(pss_args a, uint32_t rows, uint32_t max_k, bool split,
+                                           hipStream_t st, hipEvent_t split_ev) {
     const size_t esz = a.dtype == PSS_DTYPE_F16 ? 2u : 4u;
     a.vec_ok = ((a.stride * esz) % 16u == 0u) && (((uintptr_t)a.logits & 15u) == 0u) &&
                ((a.V * esz) % 16u == 0u);
     switch (pss_stream_pick_ept(a.V, rows)) {
-        case 32: return pss_stream_go<32>(a, rows, max_k, st, split);
-        default: return pss_stream_go<16>(a, rows, max_k, st, split);
+        case 32: return pss_stream_go<32>(a, rows, max_k, split, st, split_ev);
+        default: return pss_stream_go<16>(a, rows, max_k, split, st, split_ev);
     }
 }
 

@@ -14,8 +14,8 @@ from pumice_amd import workloads as WL
 
 pytestmark = pytest.mark.gpu
 
-PATHS = [0, S.ENQ_GENERAL]          # auto kernel choice, forced general kernel
-PATH_IDS = ["auto", "general"]
+PATHS = [0, S.ENQ_SPLIT, S.ENQ_GENERAL]  # fused kernel, two-kernel form, general kernel
+PATH_IDS = ["fused", "split", "general"]
 PROB_RTOL = 1e-6                    # normalized probabilities vs fp64
 
 
