@@ -8,7 +8,8 @@ A "step" is one pss_enqueue over a batch of logit rows resident in HBM.
             sampled rows/s, plus algorithmic HBM GB/s and its roofline
             fraction.  Each step reads a different one of NBUF batches, so the
             working set (>= 600 MB) exceeds the 256 MB last-level cache and
-            rows come from HBM.
+            rows come from HBM.  One step is one launch of pss_row_kernel (or, with
+            --split / --general, the other two forms).
   latency   batch 1 (config c2): launch-to-token p50/p90 (host clock, token
             stored by the kernel into pinned host memory), per-step GPU time,
             and steady decode-group us/token through the C generate loop.
@@ -30,7 +31,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
-TRAFFIC_MD = "seg_kernel_traffic_headline.md"
+TRAFFIC_MD = "row_kernel_traffic_headline.md"
 NBUF = 6
 
 
@@ -57,7 +58,11 @@ def copy_calibration(nbytes, reps=10):
 
 
 def bench_batched(w, steps, warmup, flags=0):
-    """rows/s and per-launch GPU time for workload `w` (rows x V)."""
+    """rows/s and per-launch GPU time for workload `w` (rows x V).
+
+    The default path is one kernel per step (pss_row_kernel); with
+    S.ENQ_SPLIT it is two (pss_seg_kernel, then pss_fin_kernel) and the split
+    event the library records between them times each one."""
     from pumice_amd import hip
     from pumice_amd import sampler as S
 
@@ -80,33 +85,33 @@ def bench_batched(w, steps, warmup, flags=0):
     hip.stream_sync(stream)
     hip.synchronize()
     wall = time.perf_counter() - t0
-    # per-launch GPU time with HIP events on the sampler's stream: start, the
-    # split event the library records between its two kernels, end
+    # per-launch GPU time with HIP events on the sampler's stream around each
+    # launch (and, split form, the event between its two kernels)
     n_ev = min(steps, 100)
     ev = [(hip.Event(), hip.Event(), hip.Event()) for _ in range(n_ev)]
+    split = bool(flags & S.ENQ_SPLIT)
     for i in range(n_ev):
         ev[i][0].record(stream)
-        s.enqueue(bufs[i % NBUF].ptr, dtype, w.V, w.rows, flags=flags, split_event=ev[i][1].ptr)
+        s.enqueue(bufs[i % NBUF].ptr, dtype, w.V, w.rows, flags=flags,
+                  split_event=ev[i][1].ptr if split else None)
         ev[i][2].record(stream)
     hip.stream_sync(stream)
     kt = [a.elapsed_ms(c) for a, b, c in ev]
-    seg = [a.elapsed_ms(b) for a, b, c in ev]
     res, tok = s.read_results(w.rows)
     s.close()
     for b in bufs:
         b.free()
     bpr = w.bytes_per_row()
-    seg_bpr = w.seg_bytes_per_row()
     k_ms = float(np.mean(kt))
-    seg_ms = float(np.mean(seg))
-    return dict(rows=w.rows, V=w.V, dtype=str(w.logits.dtype), ms_per_step=wall * 1e3 / steps,
-                rows_per_s=w.rows * steps / wall, step_ms_mean=k_ms, step_ms_p50=pct(kt, 50),
-                seg_kernel_ms_mean=seg_ms, fin_ms_mean=k_ms - seg_ms,
-                bytes_per_row=bpr, bytes_per_launch=bpr * w.rows,
-                seg_bytes_per_launch=seg_bpr * w.rows,
-                seg_gbps=seg_bpr * w.rows / (seg_ms * 1e-3) / 1e9,
-                step_gbps=bpr * w.rows / (k_ms * 1e-3) / 1e9,
-                wall_gbps=bpr * w.rows * steps / wall / 1e9)
+    out = dict(rows=w.rows, V=w.V, dtype=str(w.logits.dtype), ms_per_step=wall * 1e3 / steps,
+               rows_per_s=w.rows * steps / wall, launch_ms_mean=k_ms, launch_ms_p50=pct(kt, 50),
+               bytes_per_row=bpr, bytes_per_launch=bpr * w.rows,
+               launch_gbps=bpr * w.rows / (k_ms * 1e-3) / 1e9,
+               wall_gbps=bpr * w.rows * steps / wall / 1e9)
+    if split:
+        seg = [a.elapsed_ms(b) for a, b, c in ev]
+        out.update(seg_kernel_ms_mean=float(np.mean(seg)), fin_ms_mean=k_ms - float(np.mean(seg)))
+    return out
 
 
 def bench_latency(steps):
@@ -211,18 +216,15 @@ def traffic_from_pmc(fetch_dir, write_dir, out_path):
         scale = nbytes / (float(np.mean(copy)) * 1024.0)
         out[counter] = {"copy_kib": float(np.mean(copy)), "scale": scale}
         for (k, g), vs in vals.items():
-            if k.startswith("void pss_seg_kernel") or k.startswith("pss_fin_kernel"):
-                name = "seg" if "seg_kernel" in k else "fin"
-                out[counter][name + "_kib"] = float(np.mean(vs))
-                out[counter][name + "_bytes"] = float(np.mean(vs)) * 1024.0 * scale
-    seg = out["FETCH_SIZE"]["seg_bytes"] + out["WRITE_SIZE"]["seg_bytes"]
-    fin = out["FETCH_SIZE"]["fin_bytes"] + out["WRITE_SIZE"]["fin_bytes"]
+            if "pss_row_kernel" in k:
+                out[counter]["row_kib"] = float(np.mean(vs))
+                out[counter]["row_bytes"] = float(np.mean(vs)) * 1024.0 * scale
+    row = out["FETCH_SIZE"]["row_bytes"] + out["WRITE_SIZE"]["row_bytes"]
     res = {"workload": "headline 256 x 102,400 fp32", "calibration_copy_bytes": nbytes,
-           "counters": out, "seg_kernel_hbm_bytes_per_launch": seg, "fin_kernel_hbm_bytes_per_launch": fin,
-           "step_hbm_bytes_per_launch": seg + fin}
+           "counters": out, "row_kernel_hbm_bytes_per_launch": row}
     fc, wc = out["FETCH_SIZE"], out["WRITE_SIZE"]
     md = [
-        "# HBM traffic of the streaming sampler kernels, headline workload (256 x 102,400 fp32)",
+        "# HBM traffic of pss_row_kernel, headline workload (256 x 102,400 fp32)",
         "",
         "Commands (from the repository root on the MI355X box; then, on any host,",
         "`python3 bench.py --traffic-from <fetch dir> <write dir>` wrote this file):",
@@ -240,11 +242,9 @@ def traffic_from_pmc(fetch_dir, write_dir, out_path):
         "",
         "| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes per launch (scaled) |",
         "|---|---|---|---|",
-        "| pss_seg_kernel | %.1f | %.1f | %.0f |" % (fc["seg_kib"], wc["seg_kib"], seg),
-        "| pss_fin_kernel | %.1f | %.1f | %.0f |" % (fc["fin_kib"], wc["fin_kib"], fin),
+        "| pss_row_kernel | %.1f | %.1f | %.0f |" % (fc["row_kib"], wc["row_kib"], row),
         "",
-        "Algorithmic bytes per launch: segment kernel 256 x (102,400 x 4 + 4 x 64 + 28) = %d;" % (256 * (409600 + 256 + 28)),
-        "whole step 256 x (102,400 x 4 + 4 x 64 + 44) = %d." % (256 * (409600 + 256 + 44)),
+        "Algorithmic bytes per launch: 256 x (102,400 x 4 + 4 x 64 + 44) = %d." % (256 * (409600 + 256 + 44)),
         "",
         "```json",
         json.dumps(res, indent=1),
@@ -266,6 +266,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline only (c3/c4/c5 and latency skipped)")
     ap.add_argument("--general", action="store_true", help="force the general kernel")
+    ap.add_argument("--split", action="store_true", help="force the two-kernel form")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run device-to-device copies of one headline batch (traffic calibration)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -284,7 +285,8 @@ def main():
     from pumice_amd import sampler as S
     from pumice_amd import workloads as WL
 
-    flags = S.ENQ_GENERAL if args.general else 0
+    flags = S.ENQ_GENERAL if args.general else (S.ENQ_SPLIT if args.split else 0)
+    kernel = "general" if args.general else ("split" if args.split else "fused")
     log("generating headline workload")
     head = WL.headline(seed=0)
     log("headline: 256 x 102400 fp32")
@@ -316,8 +318,12 @@ def main():
             txt = f.read()
         if "```json" in txt:
             traffic = json.loads(txt.split("```json", 1)[1].split("```", 1)[0]).get(
-                "seg_kernel_hbm_bytes_per_launch")
-    achieved = h["seg_gbps"]
+                "row_kernel_hbm_bytes_per_launch")
+        if kernel != "fused":
+            traffic = None
+    # dominant (fused: only) kernel: algorithmic bytes per launch / mean
+    # per-launch time from HIP events on the sampler's stream
+    achieved = h["launch_gbps"]
     line = {
         "metric": "sampled rows/sec + HBM GB/s at V=102,400 (B=256); p50 µs/token at B=1",
         "value": h["rows_per_s"],
@@ -334,9 +340,9 @@ def main():
         "config": {
             "workload": "headline: 256 rows x V=102,400 fp32 logits, rep 1.1 + presence 0.5 over a "
                         "64-id window, T 0.8, top-k 40, top-p 0.95, min-p 0.05, xorshift32 seeds 0..255",
-            "rows": 256, "vocab": 102400, "kernel": "general" if args.general else "auto",
+            "rows": 256, "vocab": 102400, "kernel": kernel,
         },
-        "hbm_gbps": h["step_gbps"],
+        "hbm_gbps": h["wall_gbps"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic},
         "cpu_baseline": cpu,

@@ -79,12 +79,14 @@ struct pss_row_lds {
 
 /* Finisher scratch besides the candidate list. */
 struct pss_fin_small {
-    unsigned long long kept[64]; /* fast path: entries >= the K-th largest */
-    uint32_t hist[256];          /* fast path: radix digit counts */
+    unsigned long long cl[PSS_FAST_N]; /* fast path: entries at or above the row bound */
+    unsigned long long kept[64];       /* fast path: entries at or above the K-th largest */
+    uint32_t hist[256];                /* fast path: radix digit counts */
     pss_gen_shared g;
-    uint32_t mx[PSS_SEG_NW];     /* per-wave largest key */
+    uint32_t mx[PSS_SEG_NW];           /* per-wave largest key */
     uint32_t digit;
     uint32_t rem;
+    uint32_t nc;
     uint32_t nk;
     uint32_t fail;
 };
@@ -254,14 +256,18 @@ struct pss_row_pre {
 
 /*
  * Fast finisher for K <= 64 and up to PSS_FAST_N candidates (list), those
- * below the row-wide bound G ignored:
- *   1. the row's K-th largest by an LDS radix select (8-bit digits), starting
- *      at the first digit below the common prefix of G and the row maximum --
- *      every candidate that matters lies between the two;
- *   2. the <= 64 entries at or above it, one per lane of wave 0: sort by key
- *      (ties by id), scan the masses for the top-p cut, apply min-p, sort the
- *      kept set by id, scan, take the first id whose cumulative mass exceeds
- *      the draw target.  Lane exchanges are DPP / permlane (no LDS).
+ * below the row-wide bound G ignored (G is at most the K-th largest value,
+ * so every entry of the top-K is at or above it):
+ *   1. the entries at or above G are compacted into sh.cl;
+ *   2. at most 64 of them (the usual case): one per lane of wave 0, which
+ *      sorts them by (key descending, id ascending) and reads the K-th
+ *      largest key at position K - 1.  Otherwise an LDS radix select of the
+ *      K-th largest over them (8-bit digits below the common prefix of G and
+ *      the maximum), and the <= 64 entries at or above it go to wave 0;
+ *   3. wave 0, one entry per lane: scan the masses for the top-p cut, apply
+ *      min-p, sort the kept set by id, scan, take the first id whose
+ *      cumulative mass exceeds the draw target.  Lane exchanges are DPP /
+ *      permlane (no LDS).
  * Returns false (nothing written) when more than 64 entries are at or above
  * the K-th largest (heavy ties).
  */
@@ -270,91 +276,116 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
                                                      const pss_rowcfg& c, const unsigned long long* list,
                                                      uint32_t n, uint32_t G, const pss_row_pre& pre,
                                                      pss_fin_small& sh) {
-    constexpr int R = (int)(PSS_FAST_N / NT);
-    static_assert(NT >= 256 && NT <= 1024 && PSS_FAST_N % NT == 0, "radix bins: the first 256 threads");
+    constexpr int R = (int)((PSS_FAST_N + NT - 1) / NT);
+    static_assert(NT >= 256 && NT <= 1024, "radix bins: the first 256 threads");
     if (c.K > 64u || n > PSS_FAST_N) return false;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    uint64_t e[R];
-    uint32_t k[R];
-    uint32_t kmax = 0;
+    if (tid == 0) {
+        sh.nc = 0u;
+        sh.nk = 0u;
+    }
+    __syncthreads();
+    /* 1. compact */
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t i = tid + (uint32_t)r * NT;
-        e[r] = i < n ? list[i] : 0ull;
-        k[r] = (uint32_t)(e[r] >> 32);
-        if (k[r] < G) k[r] = 0u;
-        kmax = k[r] > kmax ? k[r] : kmax;
+        const unsigned long long e = i < n ? list[i] : 0ull;
+        const bool keep = i < n && (uint32_t)(e >> 32) >= G;
+        const uint64_t m = __ballot(keep);
+        if (m) {
+            uint32_t b0 = 0u;
+            if (lane == 0u) b0 = atomicAdd(&sh.nc, (uint32_t)__popcll(m));
+            const uint32_t base = __builtin_amdgcn_readfirstlane(b0);
+            if (keep)
+                sh.cl[base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u))] = e;
+        }
     }
-    kmax = wave_max_u32(kmax);
-    if (lane == 0) sh.mx[wave] = kmax;
-    if (tid == 0) sh.nk = 0;
     __syncthreads();
-    uint32_t tmaxKey = 0;
+    const uint32_t nc = sh.nc;
+    uint32_t tauK = 0u, cnt = nc;
+    const unsigned long long* src = sh.cl;
+    if (nc > 64u) {
+        /* 2b. radix select over the compacted entries */
+        uint64_t e[R];
+        uint32_t k[R];
+        uint32_t kmax = 0;
 #pragma unroll
-    for (int w = 0; w < NT / PSS_WAVE; ++w) tmaxKey = sh.mx[w] > tmaxKey ? sh.mx[w] : tmaxKey;
-
-    /* S5: radix select of the K-th largest below the common prefix */
-    const uint32_t d = G ^ tmaxKey;
-    uint32_t tauK = tmaxKey;
-    if (d) {
-        const int hibit = 31 - __clz(d);
-        int shift = (hibit / 8) * 8;
-        uint32_t pmask = shift + 8 >= 32 ? 0u : ~((1u << (shift + 8)) - 1u);
-        uint32_t prefix = tmaxKey & pmask;
-        uint32_t rem = c.K;
-        for (; shift >= 0; shift -= 8) {
-            if (tid < 256u) sh.hist[tid] = 0u;
-            __syncthreads();
+        for (int r = 0; r < R; ++r) {
+            const uint32_t i = tid + (uint32_t)r * NT;
+            e[r] = i < nc ? sh.cl[i] : 0ull;
+            k[r] = i < nc ? (uint32_t)(e[r] >> 32) : 0u;
+            kmax = k[r] > kmax ? k[r] : kmax;
+        }
+        kmax = wave_max_u32(kmax);
+        if (lane == 0) sh.mx[wave] = kmax;
+        __syncthreads();
+        uint32_t tmaxKey = 0;
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (k[r] && (k[r] & pmask) == prefix) atomicAdd(&sh.hist[(k[r] >> shift) & 255u], 1u);
-            __syncthreads();
-            if (tid < 64) {
-                const uint4 h = *(const uint4*)&sh.hist[4u * lane];
-                const uint32_t s4 = h.x + h.y + h.z + h.w;
-                const uint32_t above = (uint32_t)(wave_incl_suffix_u64(s4) - s4); /* lanes > lane */
-                if (above < rem && rem <= above + s4) {
-                    uint32_t cum = above, dg = 4u * lane;
-                    const uint32_t hv[4] = {h.x, h.y, h.z, h.w};
-                    for (int i = 3; i >= 0; --i) {
-                        if (cum + hv[i] >= rem) {
-                            dg = 4u * lane + (uint32_t)i;
-                            break;
+        for (int w = 0; w < NT / PSS_WAVE; ++w) tmaxKey = sh.mx[w] > tmaxKey ? sh.mx[w] : tmaxKey;
+        const uint32_t d = G ^ tmaxKey;
+        tauK = tmaxKey;
+        if (d) {
+            const int hibit = 31 - __clz(d);
+            int shift = (hibit / 8) * 8;
+            uint32_t pmask = shift + 8 >= 32 ? 0u : ~((1u << (shift + 8)) - 1u);
+            uint32_t prefix = tmaxKey & pmask;
+            uint32_t rem = c.K;
+            for (; shift >= 0; shift -= 8) {
+                if (tid < 256u) sh.hist[tid] = 0u;
+                __syncthreads();
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    if (k[r] && (k[r] & pmask) == prefix) atomicAdd(&sh.hist[(k[r] >> shift) & 255u], 1u);
+                __syncthreads();
+                if (tid < 64) {
+                    const uint4 h = *(const uint4*)&sh.hist[4u * lane];
+                    const uint32_t s4 = h.x + h.y + h.z + h.w;
+                    const uint32_t above = (uint32_t)(wave_incl_suffix_u64(s4) - s4); /* lanes > lane */
+                    if (above < rem && rem <= above + s4) {
+                        uint32_t cum = above, dg = 4u * lane;
+                        const uint32_t hv[4] = {h.x, h.y, h.z, h.w};
+                        for (int i = 3; i >= 0; --i) {
+                            if (cum + hv[i] >= rem) {
+                                dg = 4u * lane + (uint32_t)i;
+                                break;
+                            }
+                            cum += hv[i];
                         }
-                        cum += hv[i];
+                        sh.digit = dg;
+                        sh.rem = rem - cum;
                     }
-                    sh.digit = dg;
-                    sh.rem = rem - cum;
                 }
+                __syncthreads();
+                prefix |= sh.digit << shift;
+                pmask |= 0xFFu << shift;
+                rem = sh.rem;
             }
-            __syncthreads();
-            prefix |= sh.digit << shift;
-            pmask |= 0xFFu << shift;
-            rem = sh.rem;
+            tauK = prefix;
         }
-        tauK = prefix;
-    }
-
-    /* entries at or above the K-th largest, to wave 0 */
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-        if (k[r] && k[r] >= tauK) {
-            const uint32_t pos = atomicAdd(&sh.nk, 1u);
-            if (pos < 64u) sh.kept[pos] = e[r];
-        }
-    __syncthreads();
-    const uint32_t nK = sh.nk;
-    if (nK > 64u) return false;
+        for (int r = 0; r < R; ++r)
+            if (k[r] && k[r] >= tauK) {
+                const uint32_t pos = atomicAdd(&sh.nk, 1u);
+                if (pos < 64u) sh.kept[pos] = e[r];
+            }
+        __syncthreads();
+        cnt = sh.nk;
+        if (cnt > 64u) return false;
+        src = sh.kept;
+    }
+    if (cnt == 0u) return false;
 
     if (tid < 64) {
-        const bool valid = lane < nK;
-        const uint64_t my = valid ? sh.kept[lane] : 0ull;
-        const float tmax = pss_unkey(tmaxKey);
-
-        /* S5/S6: descending by key (ties by id), inclusive mass scan */
+        /* S5/S6: descending by key (ties by id); the K-th largest (when not
+         * selected above); inclusive mass scan */
+        const bool valid = lane < cnt;
+        const uint64_t my = valid ? src[lane] : 0ull;
         const uint64_t sx = dpp_sort_asc_u64(valid ? (((uint64_t)(~(uint32_t)(my >> 32)) << 32) | (uint32_t)my) : ~0ull);
-        const bool sv = sx != ~0ull;
         const uint32_t skey = ~(uint32_t)(sx >> 32), sid = (uint32_t)sx;
+        const uint32_t tmaxKey = wave_read_u32(skey, 0u);
+        if (nc <= 64u) tauK = wave_read_u32(skey, (c.K <= cnt ? c.K : cnt) - 1u);
+        const bool sv = sx != ~0ull && skey >= tauK;
+        const float tmax = pss_unkey(tmaxKey);
         const float sp = sv ? pss_prob(pss_unkey(skey), tmax) : 0.0f;
         const uint64_t sq = sv ? pss_fixq(sp) : 0ull;
         const uint64_t P = wave_incl_scan_u64(sq);
