@@ -1,34 +1,31 @@
 /*
- * pss_stream.h - the streaming sampler (the HBM-roofline path): two kernels
- * on the sampler's stream.
+ * pss_stream.h - the streaming sampler (the HBM-roofline path).
  *
- * pss_seg_kernel, grid (S, rows) x 256 threads: workgroup (s, r) owns
- * segment s of row r, SEG = 256 * EPT consecutive ids.  It reads the segment
- * once with 16-byte coalesced loads (4 fp32 / 8 fp16 per lane), all issued
- * before anything waits for them, and keeps the transformed logits
- * t = l * (1/T) (penalized for ids in the window, from an LDS bitmap of the
- * segment's ids) in registers.  Then:
- *   bound  every lane's top-m values (m = ceil(K / 256)) go to LDS and every
- *          wave finds the K-th largest of them with ballots.  They are
- *          elements of the segment, so every element at or above the row's
- *          K-th largest value is >= that bound; the bound is also published
- *          row-wide (atomic max, not waited for) and read back by later
- *          segments of the row to tighten theirs.
- *   pool   the elements at or above the bound (a few more than K) are
- *          appended to an LDS list and copied to the segment's own slot range
- *          of the row's pool, with their count.  No returning global atomic,
- *          no cross-workgroup wait.
- *   greedy rows store the segment's (max key, smallest id) instead.
+ * The rows are cut into items of 64 * EPT consecutive ids, processed in
+ * rounds by workgroups of PSS_SEG_NW independent waves (one item per wave per
+ * round): each item is read once with 16-byte buffer loads straight into the
+ * wave's LDS staging area, one round ahead of its compute; window ids are
+ * applied once per id by the lane that claims them; every element at or
+ * above a certified lower bound of the row's K-th largest value (from the
+ * waves' running top values, combined across the workgroup after the round's
+ * one barrier) becomes a candidate.  Two forms:
  *
- * pss_fin_kernel, one 256-thread workgroup per row, after it on the stream:
- * gathers the row's candidates (about S * K entries, L2-resident) into LDS
- * and finishes the row: exact K-th largest, masses q = trunc(exp(t - tmax) *
- * 2^45), top-p, min-p and the draw as an ascending-id inverse CDF over the
- * kept set, then the epilogue (result slot, token, window, rng, position).
- * Rows the candidates cannot finish -- top-k off or above 1024, a segment
- * whose candidates overflow its slots (heavy ties) -- run the general
- * algorithm there instead, re-reading the row.  Every path computes the same
- * bits as the one-workgroup-per-row general kernel.
+ * pss_row_kernel (default), one workgroup per row: candidates gather in an
+ * LDS list and the workgroup finishes the row itself after its last round --
+ * exact K-th largest, masses q = trunc(exp(t - tmax) * 2^45), top-p, min-p,
+ * the draw as an ascending-id inverse CDF over the kept set, the epilogue
+ * (result slot, token, window, rng, position).
+ *
+ * pss_seg_kernel + pss_fin_kernel (PSS_ENQ_SPLIT): workgroups over any range
+ * of items, candidates into per-item slots of a per-row pool in HBM (rows
+ * split across workgroups share a row-wide bound through a relaxed atomic
+ * max); then one workgroup per row gathers the candidates and runs the same
+ * finisher.
+ *
+ * Rows the candidates cannot finish (top-k off or above PSS_SEG_KMAX, a window
+ * above PSS_SEG_WMAX ids, heavy ties, an overflowing list) run the general
+ * algorithm in the finishing workgroup, re-reading the row.  Every path
+ * computes the same bits as the one-workgroup-per-row general kernel.
  */
 #ifndef PSS_STREAM_H
 #define PSS_STREAM_H

@@ -74,13 +74,6 @@ class Workload:
         W = int(min(self.params["penaltyLength"].max(), MAX_PEN))
         return self.V * self.logits.dtype.itemsize + 4 * W + 44
 
-    def seg_bytes_per_row(self):
-        """The segment kernel's share: the row, the window and the params
-        (V*elem + 4*W + 28); the finisher reads the rng and position and
-        writes the token, history slot, rng and position."""
-        W = int(min(self.params["penaltyLength"].max(), MAX_PEN))
-        return self.V * self.logits.dtype.itemsize + 4 * W + 28
-
 
 def c1(seed=0, V=V_PRUNED):
     rng = np.random.default_rng(seed)
