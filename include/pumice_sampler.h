@@ -105,10 +105,15 @@ typedef struct {
 /* Run the one-workgroup-per-row general kernel instead of the streaming kernel
  * (both compute identical results; used to cross-check them). */
 #define PSS_ENQ_GENERAL 1u
-/* Run the streaming path as two kernels (segment kernel over all rows, then a
- * finisher kernel per row) instead of the fused one-workgroup-per-row kernel
- * (identical results; used to cross-check them). */
+/* The streaming path picks its form by batch size: each row spread over a
+ * few workgroups of one round, finished by the last of them to arrive (small
+ * batches), or one workgroup per row (large).  These force a form (identical
+ * results; used to cross-check them): two kernels (segment kernel over all
+ * rows, then a finisher kernel per row), the one-workgroup-per-row kernel, or
+ * the small-batch kernel. */
 #define PSS_ENQ_SPLIT 2u
+#define PSS_ENQ_FUSED 4u
+#define PSS_ENQ_SMALL 8u
 
 /* Words per row of kept_mask. */
 uint32_t pss_mask_words(uint32_t vocab);

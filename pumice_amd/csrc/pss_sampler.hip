@@ -271,8 +271,12 @@ extern "C" pss_status pss_enqueue_ex(pss_sampler* s, const void* logits, uint32_
         uint32_t max_k = 0;
         for (uint32_t r = 0; r < rows; ++r) max_k = s->h_topk[r] > max_k ? s->h_topk[r] : max_k;
         const hipEvent_t split = opts ? (hipEvent_t)opts->split_event : NULL;
-        const bool two = opts && (opts->flags & PSS_ENQ_SPLIT);
-        if (pss_stream_launch(a, rows, max_k, two, s->stream, split) != hipSuccess) return PSS_ERR_HIP;
+        const uint32_t fl = opts ? opts->flags : 0u;
+        const int form = (fl & PSS_ENQ_SPLIT)   ? PSS_FORM_SPLIT
+                         : (fl & PSS_ENQ_FUSED) ? PSS_FORM_FUSED
+                         : (fl & PSS_ENQ_SMALL) ? PSS_FORM_SMALL
+                                                : -1;
+        if (pss_stream_launch(a, rows, max_k, form, s->stream, split) != hipSuccess) return PSS_ERR_HIP;
         return PSS_OK;
     }
     pss_general_kernel<<<dim3(rows), dim3(PSS_GEN_NT), 0, s->stream>>>(a);

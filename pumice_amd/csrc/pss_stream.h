@@ -48,18 +48,37 @@
 
 /* Per-row workspace: header, then the candidate pool. */
 struct pss_row_ws {
-    uint32_t bound; /* row-wide lower bound on the K-th largest key (max over items) */
-    uint32_t pad[15];
+    uint32_t bound;  /* row-wide lower bound on the K-th largest key (max over items) */
+    uint32_t ticket; /* small-batch form: workgroups of the row done so far */
+    uint32_t pad[30];
     uint32_t seg_count[PSS_SEG_MAX_SLOTS];          /* candidates per item, or PSS_SEG_OVERFLOW */
     unsigned long long seg_best[PSS_SEG_MAX_SLOTS]; /* greedy rows: (key << 32) | ~id per item */
 };
-static_assert(sizeof(pss_row_ws) % 64 == 0, "workspace header is a multiple of 64 bytes");
+static_assert(sizeof(pss_row_ws) % 128 == 0, "workspace header is a multiple of 128 bytes");
 #define PSS_WS_ROW_BYTES (sizeof(pss_row_ws) + (size_t)PSS_POOL_CAP * 8u)
+
+/* Pool entries per item: an equal share of the pool, a multiple of 16 (each
+ * item's range starts on a 128-byte line; at least 64 for NS <= 256). */
+__host__ __device__ __forceinline__ uint32_t pss_pool_capw(uint32_t NS) { return (PSS_POOL_CAP / NS) & ~15u; }
+#define PSS_FIN_SPEC 16u /* pool entries per item the finisher loads with the counts */
 
 static inline size_t pss_stream_ws_bytes(uint32_t rows) { return (size_t)rows * PSS_WS_ROW_BYTES; }
 
+/* Workspace accesses that other workgroups of the same launch may read:
+ * agent-scope (coherent across the XCDs' L2 caches) relaxed atomics, so a
+ * store is visible to every workgroup once the storing wave's memory counter
+ * has drained, and a load sees it without any cache maintenance. */
 __device__ __forceinline__ uint32_t pss_ld_agent(const uint32_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long pss_ld_agent64(const unsigned long long* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void pss_st_agent(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void pss_st_agent64(unsigned long long* p, unsigned long long v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -559,6 +578,30 @@ __device__ __forceinline__ void pss_wave_side_load(const pss_args& a, uint32_t r
     sd.G0 = (greedy || !with_bound) ? 0u : pss_ld_agent(&ws->bound + z);
 }
 
+/* Small-batch form: the side values loaded before the row's parameters are
+ * known (the first 4 x 64 ids of the window buffer, which holds
+ * PSS_MAX_PENALTY_LEN >= 256 per row), then trimmed to the row's window. */
+__device__ __forceinline__ void pss_wave_side_load_all(const pss_args& a, uint32_t row, pss_wave_side& sd) {
+    static_assert(PSS_MAX_PENALTY_LEN >= 4u * PSS_WAVE, "window buffer holds the ids a wave loads");
+    const uint32_t* hist_row = a.history + (size_t)row * PSS_MAX_PENALTY_LEN;
+    const uint32_t lane = pss_tid() & 63u;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) sd.hid[h] = hist_row[lane + (uint32_t)h * PSS_WAVE];
+    const pss_row_ws* ws = (const pss_row_ws*)((const char*)a.ws + (size_t)row * PSS_WS_ROW_BYTES);
+    uint32_t z = 0u;
+    __asm__ __volatile__("" : "+v"(z));
+    sd.G0 = pss_ld_agent(&ws->bound + z);
+}
+__device__ __forceinline__ void pss_wave_side_trim(const pss_args& a, const sample_params& sp, pss_wave_side& sd) {
+    const bool greedy = pss_seg_row_greedy(a, sp);
+    const uint32_t W = sp.penaltyLength < PSS_MAX_PENALTY_LEN ? sp.penaltyLength : PSS_MAX_PENALTY_LEN;
+    const uint32_t lane = pss_tid() & 63u;
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+        if (greedy || lane + (uint32_t)h * PSS_WAVE >= W) sd.hid[h] = PSS_SENTINEL;
+    if (greedy) sd.G0 = 0u;
+}
+
 /* The K-th largest (1 <= K <= 64 R) of the R keys of each of the 64 lanes,
  * to 16 bits: the largest x with at least K keys >= x, one bit per round
  * (ballots; every lane gets the same value). */
@@ -631,7 +674,7 @@ struct pss_wave_run {
  * restrict argument: the kernel's stores cannot alias it, so the row
  * parameters of later items still come through scalar loads.
  */
-template <int EPT, int DT, bool M1, bool FUSED>
+template <int EPT, int DT, bool M1, bool FUSED, bool SMALL = false>
 __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, uint32_t i0, uint32_t i1,
                                                const sample_params* __restrict__ params,
                                                pss_wave_lds<EPT, DT>* lds, unsigned long long* joint,
@@ -644,7 +687,9 @@ __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, u
     const uint32_t wave = __builtin_amdgcn_readfirstlane(pss_tid() >> 6);
     const uint32_t lane = pss_tid() & 63u;
     pss_wave_lds<EPT, DT>& wl = lds[wave];
-    if (lane == 0u) joint[wave] = ~0ull;
+    /* small form: one round over one row; idle waves hold a neutral slot */
+    if (lane == 0u)
+        joint[wave] = (SMALL && i0 + wave >= i1) ? (((unsigned long long)(i0 / NS) << 32) | 0xFFFFFFFFull) : ~0ull;
     wl.claim[lane] = 0u;
     __syncthreads();
     const uint32_t V = a.V;
@@ -659,18 +704,27 @@ __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, u
     bool act = it < i1;
     uint32_t row = act ? it / NS : i0 / NS;
     uint32_t s = act ? it - row * NS : 0u;
+    if (SMALL && act) {
+        /* loads first, parameters after: the item and window ids are in
+         * flight while the row's parameters arrive (an uncovered row's
+         * staged item is never read) */
+        pss_wave_issue<EPT, DT>(a, row, s, wl);
+        pss_wave_side_load_all(a, row, sd);
+    }
     sample_params sp = params[row];
     bool cov = act && pss_seg_row_covered(a, sp);
-    if (cov) {
+    if (SMALL) {
+        if (act) pss_wave_side_trim(a, sp, sd);
+    } else if (cov) {
         pss_wave_issue<EPT, DT>(a, row, s, wl);
         pss_wave_side_load(a, row, sp, sd, !FUSED);
     }
     for (uint32_t r = 0; r < R; ++r) {
         const uint32_t nit = it + NW;
-        const bool nact = nit < i1;
+        const bool nact = !SMALL && nit < i1;
         const uint32_t nrow = nact ? nit / NS : row;
         const uint32_t ns = nact ? nit - nrow * NS : 0u;
-        const sample_params nsp = params[nrow];
+        const sample_params nsp = SMALL ? sp : params[nrow];
         const bool ncov = nact && pss_seg_row_covered(a, nsp);
         pss_wave_side nsd = none;
 
@@ -784,7 +838,7 @@ __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, u
                     if (lane == 0u) atomicMax(&rl->best, (unsigned long long)best);
                 } else {
                     pss_row_ws* ws = (pss_row_ws*)((char*)a.ws + (size_t)row * PSS_WS_ROW_BYTES);
-                    if (lane == 0u) ws->seg_best[s] = best;
+                    if (lane == 0u) pss_st_agent64(&ws->seg_best[s], best);
                 }
             } else {
                 /* running values; fmaxf ignores NaN, which canonicalizes to
@@ -793,7 +847,9 @@ __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, u
 #pragma unroll
                 for (int i = 0; i < EPT; ++i) cur = fmaxf(cur, t[i]);
                 uint32_t T;
-                const uint32_t kq = (c.K + NW - 1u) / NW;
+                /* ceil(K / waves sharing the slots): NW, or the small form's items */
+                const uint32_t nj = SMALL ? (i1 - i0 < NW ? i1 - i0 : NW) : NW;
+                const uint32_t kq = (c.K + nj - 1u) / nj;
                 if (M1) {
                     run.top[0] = fmaxf(run.top[0], cur);
                     const uint32_t k1[1] = {pss_key(pss_canon(run.top[0]))};
@@ -868,7 +924,7 @@ __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, u
             auto id_of = [&](uint32_t i) -> uint32_t {
                 return base + (i / E) * (PSS_WAVE * E) + lane * E + (i % E);
             };
-            const uint32_t capw = FUSED ? PSS_ROW_LIST_CAP : PSS_POOL_CAP / NS;
+            const uint32_t capw = FUSED ? PSS_ROW_LIST_CAP : pss_pool_capw(NS);
             uint32_t pm = 0u, ovp = 0u;
             bool any = true;
             if (thr <= PSS_KEY_NEG_INF) {
@@ -901,17 +957,24 @@ __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, u
                 if ((FUSED ? lbase + tot <= capw : tot <= capw) && mine) {
                     unsigned long long* out = FUSED ? rl->list + lbase + (incl - mine)
                                                     : (unsigned long long*)(ws + 1) + (size_t)s * capw + (incl - mine);
+                    auto put = [&](unsigned long long v) {
+                        if (FUSED)
+                            *out = v;
+                        else
+                            pss_st_agent64(out, v);
+                        ++out;
+                    };
 #pragma unroll
                     for (int h = 0; h < 4; ++h)
-                        if ((ovp >> h) & 1u) *out++ = ((unsigned long long)pss_key(pss_canon(ov[h])) << 32) | ovid[h];
+                        if ((ovp >> h) & 1u) put(((unsigned long long)pss_key(pss_canon(ov[h])) << 32) | ovid[h]);
                     while (pm) {
                         const uint32_t i = (uint32_t)__builtin_ctz(pm);
                         pm &= pm - 1u;
-                        *out++ = ((unsigned long long)pss_key(pss_canon(pss_pick(t, i))) << 32) | id_of(i);
+                        put(((unsigned long long)pss_key(pss_canon(pss_pick(t, i))) << 32) | id_of(i));
                     }
                 }
             }
-            if (!FUSED && lane == 0u) ws->seg_count[s] = tot <= capw ? tot : PSS_SEG_OVERFLOW;
+            if (!FUSED && lane == 0u) pss_st_agent(&ws->seg_count[s], tot <= capw ? tot : PSS_SEG_OVERFLOW);
         }
         it = nit;
         row = nrow;
@@ -993,38 +1056,51 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_row_kernel(pss_args a, uint32_
 /* finisher kernel                                                           */
 /* ------------------------------------------------------------------------ */
 
-/* One workgroup per row; NS items per row were written by pss_seg_kernel. */
-__global__ void __launch_bounds__(PSS_ST_NT) pss_fin_kernel(pss_args a, uint32_t NS) {
-    constexpr int NT = PSS_ST_NT;
-    __shared__ pss_fin_shared sh;
-    __shared__ uint32_t bits[PSS_MAX_VOCAB / 32];
-    pss_globalize(a);
-    const uint32_t row = blockIdx.x, tid = threadIdx.x;
+/* Finish row `row` from its NS items in the workspace (all NT threads of the
+ * workgroup; candidates gathered into sh.list).  Everything the finish needs
+ * is requested in one round trip before anything is waited for: thread s < NS
+ * loads item s's count, its greedy best and the first PSS_FIN_SPEC entries
+ * of its pool range (an item rarely has more; the rest follow in a second
+ * trip), every thread the row-wide bound, together with the row's parameters
+ * and state.  Workspace reads are agent-scope (written by other workgroups
+ * of the same launch in the small-batch form). */
+template <int NT>
+__device__ __forceinline__ void pss_fin_row(const pss_args& a, uint32_t row, uint32_t NS, pss_fin_shared& sh,
+                                            uint32_t* bits, uint32_t bit_words) {
+    static_assert(NT >= PSS_SEG_MAX_SLOTS, "one thread per item");
+    const uint32_t tid = pss_tid();
+    pss_row_ws* ws = (pss_row_ws*)((char*)a.ws + (size_t)row * PSS_WS_ROW_BYTES);
+    const uint32_t capw = pss_pool_capw(NS);
+    const bool slot = tid < NS;
+    const unsigned long long* src = (const unsigned long long*)(ws + 1) + (size_t)(slot ? tid : 0u) * capw;
+    uint32_t ns = 0u;
+    uint64_t best = 0u;
+    unsigned long long v[PSS_FIN_SPEC];
+    if (slot) {
+        ns = pss_ld_agent(&ws->seg_count[tid]);
+        best = pss_ld_agent64(&ws->seg_best[tid]);
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < PSS_FIN_SPEC; ++u) v[u] = slot ? pss_ld_agent64(src + u) : 0ull;
+    uint32_t z = 0u;
+    __asm__ __volatile__("" : "+v"(z));
+    const uint32_t G = pss_ld_agent(&ws->bound + z);
     const uint32_t V = a.V;
     const sample_params sp = a.params[row];
-    const bool greedy = (a.mode == PSS_MODE_GREEDY) || !(sp.temperature > 0.0f);
-    const pss_rowcfg c = pss_make_rowcfg(sp, V);
-    pss_row_ws* ws = (pss_row_ws*)((char*)a.ws + (size_t)row * PSS_WS_ROW_BYTES);
     pss_row_pre pre;
     pre.rng = a.rng[row];
     pre.step = a.step[row];
     pre.pos = a.position[row];
+    const bool greedy = (a.mode == PSS_MODE_GREEDY) || !(sp.temperature > 0.0f);
+    const pss_rowcfg c = pss_make_rowcfg(sp, V);
 
     if (greedy) {
-        uint64_t best = 0;
-        for (uint32_t s = tid; s < NS; s += NT) best = ws->seg_best[s] > best ? ws->seg_best[s] : best;
         best = block_max_u64<NT>(best, sh.f.g.red);
         pss_greedy_finish<NT>(a, row, best);
         return;
     }
     bool general = !pss_seg_row_covered(a, sp);
     if (!general) {
-        /* Gather: slot counts in one round trip, their prefix sums, then each
-         * slot's owner thread copies its entries to the LDS list at its
-         * offset (the entries in one more round trip). */
-        const uint32_t G = ws->bound;
-        const uint32_t capw = PSS_POOL_CAP / NS;
-        const uint32_t ns = tid < NS ? ws->seg_count[tid] : 0u;
         const bool over = ns == PSS_SEG_OVERFLOW;
         const uint32_t n0 = over ? 0u : ns;
         if (tid == 0) sh.f.fail = 0;
@@ -1033,14 +1109,16 @@ __global__ void __launch_bounds__(PSS_ST_NT) pss_fin_kernel(pss_args a, uint32_t
         if (over) sh.f.fail = 1u;
         const uint32_t total = (uint32_t)total64;
         if (n0 && total <= PSS_FIN_LIST_CAP) {
-            const unsigned long long* src = (const unsigned long long*)(ws + 1) + (size_t)tid * capw;
-            for (uint32_t i0 = 0; i0 < n0; i0 += 8u) {
-                unsigned long long v[8];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) v[u] = i0 + u < n0 ? src[i0 + u] : 0ull;
+            for (uint32_t u = 0; u < PSS_FIN_SPEC; ++u)
+                if (u < n0) sh.list[off + u] = v[u];
+            for (uint32_t i0 = PSS_FIN_SPEC; i0 < n0; i0 += 8u) {
+                unsigned long long w[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) w[u] = i0 + u < n0 ? pss_ld_agent64(src + i0 + u) : 0ull;
 #pragma unroll
                 for (int u = 0; u < 8; ++u)
-                    if (i0 + u < n0) sh.list[off + i0 + u] = v[u];
+                    if (i0 + u < n0) sh.list[off + i0 + u] = w[u];
             }
         }
         __syncthreads();
@@ -1050,9 +1128,61 @@ __global__ void __launch_bounds__(PSS_ST_NT) pss_fin_kernel(pss_args a, uint32_t
              * list; they are below the K-th largest and never selected */
             pss_list_finish<NT>(a, row, c, sh.list, total, sh.f.g);
         }
-        if (tid == 0) ws->bound = 0u; /* for the next launch */
+        if (tid == 0) pss_st_agent(&ws->bound, 0u); /* for the next launch */
     }
-    if (general) pss_general_row<NT>(a, row, sh.f.g, bits, PSS_MAX_VOCAB / 32);
+    if (general) pss_general_row<NT>(a, row, sh.f.g, bits, bit_words);
+}
+
+/* One workgroup per row; NS items per row were written by pss_seg_kernel. */
+__global__ void __launch_bounds__(PSS_ST_NT) pss_fin_kernel(pss_args a, uint32_t NS) {
+    __shared__ pss_fin_shared sh;
+    __shared__ uint32_t bits[PSS_MAX_VOCAB / 32];
+    pss_globalize(a);
+    pss_fin_row<PSS_ST_NT>(a, blockIdx.x, NS, sh, bits, PSS_MAX_VOCAB / 32);
+}
+
+/*
+ * Small-batch form: GW workgroups per row (grid rows x GW), workgroup g of a
+ * row takes items [g NS / GW, (g + 1) NS / GW) of that row only, at most
+ * PSS_SEG_NW, in one round (each wave one item, the joint certificate over
+ * the workgroup's items).  Pool entries and counts are agent-scope stores;
+ * every wave waits for its stores to complete, then the workgroup counts
+ * itself on the row's ticket (agent-scope atomic), and the workgroup that
+ * completes the count resets it and finishes the row in place (pss_fin_row,
+ * its scratch over the staging area).  One kernel, no cache-flushing fence,
+ * no workgroup waits for another.
+ */
+template <int EPT, int DT>
+union pss_small_scratch {
+    pss_wave_lds<EPT, DT> st[PSS_SEG_NW];
+    struct {
+        pss_fin_shared fs;
+        uint32_t bits[PSS_ROW_BITS];
+    } fin;
+};
+
+template <int EPT, int DT, bool M1>
+__global__ void __launch_bounds__(PSS_SEG_NT) pss_small_kernel(pss_args a, uint32_t NS, uint32_t GW,
+                                                               const sample_params* __restrict__ params) {
+    __shared__ pss_small_scratch<EPT, DT> U;
+    __shared__ unsigned long long joint[PSS_SEG_NW];
+    __shared__ uint32_t last;
+    pss_globalize(a);
+    const uint32_t row = blockIdx.x / GW, g = blockIdx.x - row * GW;
+    const uint32_t s0 = g * NS / GW, s1 = (g + 1u) * NS / GW;
+    const uint32_t tid = pss_tid();
+    pss_seg_rounds<EPT, DT, M1, false, true>(a, NS, row * NS + s0, row * NS + s1, params, U.st, joint, nullptr);
+    pss_wait_mem(); /* this wave's pool stores, counts and staged loads have completed */
+    __syncthreads();
+    if (tid == 0u) {
+        pss_row_ws* ws = (pss_row_ws*)((char*)a.ws + (size_t)row * PSS_WS_ROW_BYTES);
+        const bool l = atomicAdd(&ws->ticket, 1u) == GW - 1u;
+        if (l) pss_st_agent(&ws->ticket, 0u); /* every other workgroup of the row has counted */
+        last = l ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!last) return;
+    pss_fin_row<PSS_SEG_NT>(a, row, NS, U.fin.fs, U.fin.bits, PSS_ROW_BITS);
 }
 
 /* ---------------------------------------------------------------------- */
@@ -1098,15 +1228,41 @@ static inline hipError_t pss_seg_launch(const pss_args& a, uint32_t NS, uint32_t
     return hipGetLastError();
 }
 
+/* Streaming forms: fused (one workgroup per row), small-batch (each row over
+ * ceil(NS / PSS_SEG_NW) workgroups of one round, finished by the last to
+ * arrive), split (two kernels). */
+enum { PSS_FORM_FUSED = 0, PSS_FORM_SMALL = 1, PSS_FORM_SPLIT = 2 };
+
+static inline uint32_t pss_small_gw(uint32_t NS) { return (NS + PSS_SEG_NW - 1u) / PSS_SEG_NW; }
+
 template <int EPT>
-static inline hipError_t pss_stream_go(const pss_args& a, uint32_t rows, uint32_t max_k, bool split,
+static inline hipError_t pss_stream_go(const pss_args& a, uint32_t rows, uint32_t max_k, int form,
                                        hipStream_t st, hipEvent_t split_ev) {
     const uint32_t item = (uint32_t)PSS_WAVE * EPT;
     const uint32_t NS = (a.V + item - 1u) / item;
     if (NS > PSS_SEG_MAX_SLOTS || (uint64_t)rows * NS >= (1ull << 31)) return hipErrorInvalidValue;
     const bool m1 = max_k <= (uint32_t)PSS_WAVE;
     hipError_t e;
-    if (!split) {
+    if (form == PSS_FORM_SMALL) {
+        const uint32_t GW = pss_small_gw(NS);
+        if ((uint64_t)rows * GW > 0x7FFFFFFFull) return hipErrorInvalidValue;
+        const dim3 grid(rows * GW), block(PSS_SEG_NT);
+        if (a.dtype == PSS_DTYPE_F16) {
+            if (m1)
+                pss_small_kernel<EPT, PSS_DTYPE_F16, true><<<grid, block, 0, st>>>(a, NS, GW, a.params);
+            else
+                pss_small_kernel<EPT, PSS_DTYPE_F16, false><<<grid, block, 0, st>>>(a, NS, GW, a.params);
+        } else {
+            if (m1)
+                pss_small_kernel<EPT, PSS_DTYPE_F32, true><<<grid, block, 0, st>>>(a, NS, GW, a.params);
+            else
+                pss_small_kernel<EPT, PSS_DTYPE_F32, false><<<grid, block, 0, st>>>(a, NS, GW, a.params);
+        }
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (split_ev && (e = hipEventRecord(split_ev, st)) != hipSuccess) return e;
+        return hipSuccess;
+    }
+    if (form == PSS_FORM_FUSED) {
         const dim3 grid(rows), block(PSS_SEG_NT);
         if (a.dtype == PSS_DTYPE_F16) {
             if (m1)
@@ -1136,17 +1292,42 @@ static inline hipError_t pss_stream_go(const pss_args& a, uint32_t rows, uint32_
     return hipGetLastError();
 }
 
+/* Resident workgroups of the small-batch kernel on the current device (one
+ * per CU at its LDS footprint), cached; 0 if unknown. */
+static inline uint32_t pss_small_capacity() {
+    static uint32_t cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+    if (dev < 64 && cache[dev]) return cache[dev];
+    int cus = 0, nb = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, pss_small_kernel<32, PSS_DTYPE_F32, true>,
+                                                     PSS_SEG_NT, 0) != hipSuccess)
+        return 0;
+    const uint32_t cap = (uint32_t)(nb > 0 ? nb : 1) * (uint32_t)(cus > 0 ? cus : 1);
+    if (dev < 64) cache[dev] = cap;
+    return cap;
+}
+
 /* max_k: the largest top-k of the launched rows (an upper bound is enough).
- * split: the two-kernel form (segment kernel + finisher kernel) instead of
- * the fused one; both compute the same bits. */
-static inline hipError_t pss_stream_launch(pss_args a, uint32_t rows, uint32_t max_k, bool split,
+ * form: PSS_FORM_*, or -1 to choose: the small-batch form while its grid is
+ * at most one pass of resident workgroups (every row spread over several CUs,
+ * one round), the fused form above that.  All forms compute the same bits. */
+static inline hipError_t pss_stream_launch(pss_args a, uint32_t rows, uint32_t max_k, int form,
                                            hipStream_t st, hipEvent_t split_ev) {
     const size_t esz = a.dtype == PSS_DTYPE_F16 ? 2u : 4u;
     a.vec_ok = ((a.stride * esz) % 16u == 0u) && (((uintptr_t)a.logits & 15u) == 0u) &&
                ((a.V * esz) % 16u == 0u);
-    switch (pss_stream_pick_ept(a.V, rows)) {
-        case 32: return pss_stream_go<32>(a, rows, max_k, split, st, split_ev);
-        default: return pss_stream_go<16>(a, rows, max_k, split, st, split_ev);
+    const int ept = pss_stream_pick_ept(a.V, rows);
+    if (form < 0) {
+        const uint64_t item = (uint64_t)PSS_WAVE * ept;
+        const uint32_t NS = (uint32_t)((a.V + item - 1u) / item);
+        const uint64_t cap = pss_small_capacity();
+        form = (cap && (uint64_t)rows * pss_small_gw(NS) <= cap) ? PSS_FORM_SMALL : PSS_FORM_FUSED;
+    }
+    switch (ept) {
+        case 32: return pss_stream_go<32>(a, rows, max_k, form, st, split_ev);
+        default: return pss_stream_go<16>(a, rows, max_k, form, st, split_ev);
     }
 }
 

@@ -29,6 +29,8 @@ RNG_XORSHIFT32, RNG_PHILOX = 0, 1
 INFO_GREEDY, INFO_FALLBACK = 1, 2
 ENQ_GENERAL = 1
 ENQ_SPLIT = 2
+ENQ_FUSED = 4
+ENQ_SMALL = 8
 
 STATUS = {0: "ok", 1: "invalid argument", 2: "allocation failed", 3: "HIP runtime error",
           4: "unsupported", 5: "no gfx950 device"}

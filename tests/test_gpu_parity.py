@@ -14,8 +14,8 @@ from pumice_amd import workloads as WL
 
 pytestmark = pytest.mark.gpu
 
-PATHS = [0, S.ENQ_SPLIT, S.ENQ_GENERAL]  # fused kernel, two-kernel form, general kernel
-PATH_IDS = ["fused", "split", "general"]
+PATHS = [0, S.ENQ_FUSED, S.ENQ_SMALL, S.ENQ_SPLIT, S.ENQ_GENERAL]  # auto form, fused, small-batch, two-kernel, general
+PATH_IDS = ["auto", "fused", "small", "split", "general"]
 PROB_RTOL = 1e-6                    # normalized probabilities vs fp64
 
 
