@@ -102,6 +102,8 @@ struct pss_fin_small {
     uint32_t mx[PSS_SEG_NW];           /* per-wave largest key */
     uint32_t digit;
     uint32_t rem;
+    uint32_t cum;
+    uint32_t hd;
     uint32_t nc;
     uint32_t nk;
     uint32_t fail;
@@ -276,14 +278,18 @@ struct pss_row_pre {
  * so every entry of the top-K is at or above it):
  *   1. the entries at or above G are compacted into sh.cl;
  *   2. at most 64 of them (the usual case): one per lane of wave 0, which
- *      sorts them by (key descending, id ascending) and reads the K-th
- *      largest key at position K - 1.  Otherwise an LDS radix select of the
- *      K-th largest over them (8-bit digits below the common prefix of G and
- *      the maximum), and the <= 64 entries at or above it go to wave 0;
- *   3. wave 0, one entry per lane: scan the masses for the top-p cut, apply
- *      min-p, sort the kept set by id, scan, take the first id whose
- *      cumulative mass exceeds the draw target.  Lane exchanges are DPP /
- *      permlane (no LDS).
+ *      sorts their keys in descending order and reads the K-th largest at
+ *      position K - 1.  Otherwise an LDS radix select over them (8-bit
+ *      digits below the common prefix of G and the maximum), which stops at
+ *      the first digit whose floor has at most 64 entries at or above it
+ *      (then wave 0's sort finds the K-th largest among them) or ends at
+ *      the K-th largest itself; the <= 64 entries at or above the result go
+ *      to wave 0;
+ *   3. wave 0, one entry per lane: scan the masses in key order for the
+ *      top-p cut, apply min-p, sort the kept ids, fetch their masses from
+ *      the owning lanes, scan, take the first id whose cumulative mass
+ *      exceeds the draw target.  Lane exchanges are DPP / permlane /
+ *      bpermute.
  * Returns false (nothing written) when more than 64 entries are at or above
  * the K-th largest (heavy ties).
  */
@@ -296,6 +302,9 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
     static_assert(NT >= 256 && NT <= 1024, "radix bins: the first 256 threads");
     if (c.K > 64u || n > PSS_FAST_N) return false;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    /* the draw depends on the row state only: off the serial tail */
+    uint32_t newRng;
+    const uint32_t u24 = pss_draw_u24_pre(a.rng_mode, pre.rng, pre.step, row, &newRng);
     if (tid == 0) {
         sh.nc = 0u;
         sh.nk = 0u;
@@ -319,6 +328,7 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
     __syncthreads();
     const uint32_t nc = sh.nc;
     uint32_t tauK = 0u, cnt = nc;
+    bool coarse = false; /* tauK is a floor below the K-th largest (at most 64 entries at or above it) */
     const unsigned long long* src = sh.cl;
     if (nc > 64u) {
         /* 2b. radix select over the compacted entries */
@@ -345,7 +355,7 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
             int shift = (hibit / 8) * 8;
             uint32_t pmask = shift + 8 >= 32 ? 0u : ~((1u << (shift + 8)) - 1u);
             uint32_t prefix = tmaxKey & pmask;
-            uint32_t rem = c.K;
+            uint32_t rem = c.K, nab = 0u;
             for (; shift >= 0; shift -= 8) {
                 if (tid < 256u) sh.hist[tid] = 0u;
                 __syncthreads();
@@ -358,23 +368,36 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
                     const uint32_t s4 = h.x + h.y + h.z + h.w;
                     const uint32_t above = (uint32_t)(wave_incl_suffix_u64(s4) - s4); /* lanes > lane */
                     if (above < rem && rem <= above + s4) {
-                        uint32_t cum = above, dg = 4u * lane;
+                        uint32_t cum = above, dg = 4u * lane, hd = 0u;
                         const uint32_t hv[4] = {h.x, h.y, h.z, h.w};
                         for (int i = 3; i >= 0; --i) {
                             if (cum + hv[i] >= rem) {
                                 dg = 4u * lane + (uint32_t)i;
+                                hd = hv[i];
                                 break;
                             }
                             cum += hv[i];
                         }
                         sh.digit = dg;
                         sh.rem = rem - cum;
+                        sh.cum = cum;
+                        sh.hd = hd;
                     }
                 }
                 __syncthreads();
                 prefix |= sh.digit << shift;
                 pmask |= 0xFFu << shift;
                 rem = sh.rem;
+                /* entries at or above the digit's floor: those above the
+                 * prefix, the larger digits, the digit's own.  At most 64
+                 * (and at least K): they go to wave 0, whose sort gives the
+                 * exact K-th largest. */
+                const uint32_t nge = nab + sh.cum + sh.hd;
+                if (nge <= 64u) {
+                    coarse = true;
+                    break;
+                }
+                nab += sh.cum;
             }
             tauK = prefix;
         }
@@ -392,18 +415,18 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
     if (cnt == 0u) return false;
 
     if (tid < 64) {
-        /* S5/S6: descending by key (ties by id); the K-th largest (when not
-         * selected above); inclusive mass scan */
         const bool valid = lane < cnt;
         const uint64_t my = valid ? src[lane] : 0ull;
-        const uint64_t sx = dpp_sort_asc_u64(valid ? (((uint64_t)(~(uint32_t)(my >> 32)) << 32) | (uint32_t)my) : ~0ull);
-        const uint32_t skey = ~(uint32_t)(sx >> 32), sid = (uint32_t)sx;
+        const uint32_t mkey = (uint32_t)(my >> 32), mid = (uint32_t)my;
+        /* S5/S6 over the keys in descending order (keys of entries are at
+         * least key(-inf) > 0; missing lanes sort last as key 0).  Every
+         * quantity here depends on the key alone, so ties need no order. */
+        const uint32_t skey = ~dpp_sort_asc_u32(valid ? ~mkey : 0xFFFFFFFFu);
         const uint32_t tmaxKey = wave_read_u32(skey, 0u);
-        if (nc <= 64u) tauK = wave_read_u32(skey, (c.K <= cnt ? c.K : cnt) - 1u);
-        const bool sv = sx != ~0ull && skey >= tauK;
+        if (nc <= 64u || coarse) tauK = wave_read_u32(skey, (c.K <= cnt ? c.K : cnt) - 1u);
+        const bool sv = valid && skey >= tauK;
         const float tmax = pss_unkey(tmaxKey);
-        const float sp = sv ? pss_prob(pss_unkey(skey), tmax) : 0.0f;
-        const uint64_t sq = sv ? pss_fixq(sp) : 0ull;
+        const uint64_t sq = sv ? pss_fixq(pss_prob(pss_unkey(skey), tmax)) : 0ull;
         const uint64_t P = wave_incl_scan_u64(sq);
         const uint64_t zk = wave_read_u64(P, 63);
         uint32_t tau = tauK;
@@ -413,25 +436,29 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
             const uint32_t tauP = wave_read_u32(skey, (uint32_t)__ffsll((long long)m) - 1u);
             tau = tauP > tau ? tauP : tau;
         }
-        /* S7 */
-        const bool kp = sv && skey >= tau && (!c.useMinP || sp >= c.minP);
-        const uint64_t kq = kp ? sq : 0ull;
+        /* S7 on each lane's own entry */
+        const float sp = valid ? pss_prob(pss_unkey(mkey), tmax) : 0.0f;
+        const bool kp = valid && mkey >= tau && (!c.useMinP || sp >= c.minP);
+        const uint64_t kq = kp ? pss_fixq(sp) : 0ull;
         const uint64_t Z = wave_sum_u64(kq);
         const uint32_t keptCount = (uint32_t)__popcll(__ballot(kp));
-        const uint32_t lastAll = wave_max_u32(kp ? sid + 1u : 0u);
+        const uint32_t lastAll = wave_max_u32(kp ? mid + 1u : 0u);
+        const uint32_t sid = mid;
 
-        /* S8: kept entries in id order ((id << 46) | q: ids < 2^18, q <= 2^45),
-         * cumulative mass, first crossing */
-        uint32_t newRng;
-        const uint32_t u24 = pss_draw_u24_pre(a.rng_mode, pre.rng, pre.step, row, &newRng);
+        /* S8: kept entries in id order ((id << 6) | lane: ids < 2^18), their
+         * masses fetched from the owning lanes, cumulative mass, first
+         * crossing */
         const uint64_t target = pss_draw_target(u24, Z);
-        const uint64_t ix = dpp_sort_asc_u64(kp ? (((uint64_t)sid << 46) | kq) : ~0ull);
-        const bool iv = ix != ~0ull;
-        const uint64_t C = wave_incl_scan_u64(iv ? (ix & ((1ull << 46) - 1ull)) : 0ull);
+        const uint32_t ix = dpp_sort_asc_u32(kp ? ((mid << 6) | lane) : 0xFFFFFFFFu);
+        const bool iv = ix != 0xFFFFFFFFu;
+        const int from = (int)((ix & 63u) << 2);
+        const uint32_t qlo = (uint32_t)__builtin_amdgcn_ds_bpermute(from, (int)(uint32_t)kq);
+        const uint32_t qhi = (uint32_t)__builtin_amdgcn_ds_bpermute(from, (int)(uint32_t)(kq >> 32));
+        const uint64_t C = wave_incl_scan_u64(iv ? (((uint64_t)qhi << 32) | qlo) : 0ull);
         const uint64_t hit = __ballot(iv && C > target);
         uint32_t tok, flags = 0;
         if (hit) {
-            tok = (uint32_t)(wave_read_u64(ix, (uint32_t)__ffsll((long long)hit) - 1u) >> 46);
+            tok = wave_read_u32(ix, (uint32_t)__ffsll((long long)hit) - 1u) >> 6;
         } else {
             tok = lastAll > 0u ? lastAll - 1u : 0u;
             flags |= PSS_INFO_FALLBACK;
