@@ -107,6 +107,7 @@ struct pss_fin_small {
     uint32_t nc;
     uint32_t nk;
     uint32_t fail;
+    uint64_t gtot; /* finisher gather totals (overflowed, not filtered, entries) */
 };
 
 struct pss_fin_shared {
@@ -276,7 +277,9 @@ struct pss_row_pre {
  * Fast finisher for K <= 64 and up to PSS_FAST_N candidates (list), those
  * below the row-wide bound G ignored (G is at most the K-th largest value,
  * so every entry of the top-K is at or above it):
- *   1. the entries at or above G are compacted into sh.cl;
+ *   1. the entries at or above G are compacted into sh.cl (unless the
+ *      caller gathered only such entries: `compacted`, with sh.nk zeroed
+ *      before its last barrier);
  *   2. at most 64 of them (the usual case): one per lane of wave 0, which
  *      sorts their keys in descending order and reads the K-th largest at
  *      position K - 1.  Otherwise an LDS radix select over them (8-bit
@@ -297,7 +300,7 @@ template <int NT>
 __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t row,
                                                      const pss_rowcfg& c, const unsigned long long* list,
                                                      uint32_t n, uint32_t G, const pss_row_pre& pre,
-                                                     pss_fin_small& sh) {
+                                                     pss_fin_small& sh, bool compacted = false) {
     constexpr int R = (int)((PSS_FAST_N + NT - 1) / NT);
     static_assert(NT >= 256 && NT <= 1024, "radix bins: the first 256 threads");
     if (c.K > 64u || n > PSS_FAST_N) return false;
@@ -305,31 +308,36 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
     /* the draw depends on the row state only: off the serial tail */
     uint32_t newRng;
     const uint32_t u24 = pss_draw_u24_pre(a.rng_mode, pre.rng, pre.step, row, &newRng);
-    if (tid == 0) {
-        sh.nc = 0u;
-        sh.nk = 0u;
-    }
-    __syncthreads();
-    /* 1. compact */
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const uint32_t i = tid + (uint32_t)r * NT;
-        const unsigned long long e = i < n ? list[i] : 0ull;
-        const bool keep = i < n && (uint32_t)(e >> 32) >= G;
-        const uint64_t m = __ballot(keep);
-        if (m) {
-            uint32_t b0 = 0u;
-            if (lane == 0u) b0 = atomicAdd(&sh.nc, (uint32_t)__popcll(m));
-            const uint32_t base = __builtin_amdgcn_readfirstlane(b0);
-            if (keep)
-                sh.cl[base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u))] = e;
+    uint32_t nc = n;
+    const unsigned long long* cl = list;
+    if (!compacted) {
+        if (tid == 0) {
+            sh.nc = 0u;
+            sh.nk = 0u;
         }
+        __syncthreads();
+        /* 1. compact */
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t i = tid + (uint32_t)r * NT;
+            const unsigned long long e = i < n ? list[i] : 0ull;
+            const bool keep = i < n && (uint32_t)(e >> 32) >= G;
+            const uint64_t m = __ballot(keep);
+            if (m) {
+                uint32_t b0 = 0u;
+                if (lane == 0u) b0 = atomicAdd(&sh.nc, (uint32_t)__popcll(m));
+                const uint32_t base = __builtin_amdgcn_readfirstlane(b0);
+                if (keep)
+                    sh.cl[base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u))] = e;
+            }
+        }
+        __syncthreads();
+        nc = sh.nc;
+        cl = sh.cl;
     }
-    __syncthreads();
-    const uint32_t nc = sh.nc;
     uint32_t tauK = 0u, cnt = nc;
     bool coarse = false; /* tauK is a floor below the K-th largest (at most 64 entries at or above it) */
-    const unsigned long long* src = sh.cl;
+    const unsigned long long* src = cl;
     if (nc > 64u) {
         /* 2b. radix select over the compacted entries */
         uint64_t e[R];
@@ -338,7 +346,7 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint32_t i = tid + (uint32_t)r * NT;
-            e[r] = i < nc ? sh.cl[i] : 0ull;
+            e[r] = i < nc ? cl[i] : 0ull;
             k[r] = i < nc ? (uint32_t)(e[r] >> 32) : 0u;
             kmax = k[r] > kmax ? k[r] : kmax;
         }
@@ -1087,28 +1095,40 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_row_kernel(pss_args a, uint32_
  * workgroup; candidates gathered into sh.list).  Everything the finish needs
  * is requested in one round trip before anything is waited for: thread s < NS
  * loads item s's count, its greedy best and the first PSS_FIN_SPEC entries
- * of its pool range (an item rarely has more; the rest follow in a second
- * trip), every thread the row-wide bound, together with the row's parameters
- * and state.  Workspace reads are agent-scope (written by other workgroups
- * of the same launch in the small-batch form). */
+ * of its pool range (one 128-byte line; an item rarely has more, the rest
+ * follow in a second trip), every thread the row-wide bound G, together with
+ * the row's parameters and state.  Of the first PSS_FIN_SPEC entries only
+ * those at or above G are gathered; when no item had more, the list is
+ * already compacted for the finisher.  Workspace reads are agent-scope
+ * (written by other workgroups of the same launch in the small-batch form). */
+#define PSS_SC1 16 /* buffer-load cache policy: device-scope coherent (sc1) */
 template <int NT>
 __device__ __forceinline__ void pss_fin_row(const pss_args& a, uint32_t row, uint32_t NS, pss_fin_shared& sh,
                                             uint32_t* bits, uint32_t bit_words) {
     static_assert(NT >= PSS_SEG_MAX_SLOTS, "one thread per item");
+    static_assert(PSS_FIN_SPEC == 16u, "one 128-byte line per item");
     const uint32_t tid = pss_tid();
     pss_row_ws* ws = (pss_row_ws*)((char*)a.ws + (size_t)row * PSS_WS_ROW_BYTES);
     const uint32_t capw = pss_pool_capw(NS);
     const bool slot = tid < NS;
-    const unsigned long long* src = (const unsigned long long*)(ws + 1) + (size_t)(slot ? tid : 0u) * capw;
+    const unsigned long long* pool = (const unsigned long long*)(ws + 1);
+    const __amdgpu_buffer_rsrc_t prs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)pool, (short)0, (int)(PSS_POOL_CAP * 8u), PSS_BUF_DW3);
+    /* threads without an item read beyond the resource: zeros, no access */
+    const uint32_t voff = slot ? tid * capw * 8u : PSS_POOL_CAP * 8u;
     uint32_t ns = 0u;
     uint64_t best = 0u;
-    unsigned long long v[PSS_FIN_SPEC];
     if (slot) {
         ns = pss_ld_agent(&ws->seg_count[tid]);
         best = pss_ld_agent64(&ws->seg_best[tid]);
     }
+    unsigned long long v[PSS_FIN_SPEC];
 #pragma unroll
-    for (uint32_t u = 0; u < PSS_FIN_SPEC; ++u) v[u] = slot ? pss_ld_agent64(src + u) : 0ull;
+    for (int j = 0; j < (int)PSS_FIN_SPEC / 2; ++j) {
+        const uint4 w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(prs, (int)(voff + 16u * j), 0, PSS_SC1));
+        v[2 * j] = ((unsigned long long)w.y << 32) | w.x;
+        v[2 * j + 1] = ((unsigned long long)w.w << 32) | w.z;
+    }
     uint32_t z = 0u;
     __asm__ __volatile__("" : "+v"(z));
     const uint32_t G = pss_ld_agent(&ws->bound + z);
@@ -1130,27 +1150,48 @@ __device__ __forceinline__ void pss_fin_row(const pss_args& a, uint32_t row, uin
     if (!general) {
         const bool over = ns == PSS_SEG_OVERFLOW;
         const uint32_t n0 = over ? 0u : ns;
-        if (tid == 0) sh.f.fail = 0;
-        uint64_t total64;
-        const uint32_t off = (uint32_t)block_excl_scan_u64<NT>(n0, sh.f.g.red, &total64);
-        if (over) sh.f.fail = 1u;
-        const uint32_t total = (uint32_t)total64;
-        if (n0 && total <= PSS_FIN_LIST_CAP) {
+        uint32_t keep = 0u;
+#pragma unroll
+        for (uint32_t u = 0; u < PSS_FIN_SPEC; ++u)
+            keep |= (u < n0 && (uint32_t)(v[u] >> 32) >= G) ? 1u << u : 0u;
+        const uint32_t extra = n0 > PSS_FIN_SPEC ? n0 - PSS_FIN_SPEC : 0u;
+        /* (overflowed items << 54) | (entries not filtered << 32) | entries
+         * written: sums of at most 256 items stay within their fields */
+        const uint64_t mine = over ? (1ull << 54) : (((uint64_t)extra << 32) | (uint64_t)(__popc(keep) + extra));
+        uint64_t off64 = 0u, tot64 = 0u;
+        if (tid == 0) sh.f.nk = 0u;
+        if (NS <= (uint32_t)PSS_WAVE) {
+            /* every item in wave 0: a wave scan, no barrier */
+            if (tid < PSS_WAVE) {
+                const uint64_t incl = wave_incl_scan_u64(mine);
+                off64 = incl - mine;
+                tot64 = wave_read_u64(incl, 63);
+            }
+        } else {
+            off64 = block_excl_scan_u64<NT>(mine, sh.f.g.red, &tot64);
+        }
+        const uint32_t off = (uint32_t)off64;
+        if (slot && (uint32_t)tot64 <= PSS_FIN_LIST_CAP) {
+            uint32_t o = off;
 #pragma unroll
             for (uint32_t u = 0; u < PSS_FIN_SPEC; ++u)
-                if (u < n0) sh.list[off + u] = v[u];
+                if ((keep >> u) & 1u) sh.list[o++] = v[u];
             for (uint32_t i0 = PSS_FIN_SPEC; i0 < n0; i0 += 8u) {
                 unsigned long long w[8];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) w[u] = i0 + u < n0 ? pss_ld_agent64(src + i0 + u) : 0ull;
+                for (int u = 0; u < 8; ++u) w[u] = i0 + u < n0 ? pss_ld_agent64(pool + (size_t)tid * capw + i0 + u) : 0ull;
 #pragma unroll
                 for (int u = 0; u < 8; ++u)
-                    if (i0 + u < n0) sh.list[off + i0 + u] = w[u];
+                    if (i0 + u < n0) sh.list[o++] = w[u];
             }
         }
+        if (tid == 0) sh.f.gtot = tot64;
         __syncthreads();
-        general = sh.f.fail != 0u || total > PSS_FIN_LIST_CAP;
-        if (!general && !pss_list_finish_fast<NT>(a, row, c, sh.list, total, G, pre, sh.f)) {
+        tot64 = sh.f.gtot;
+        const uint32_t total = (uint32_t)tot64;
+        const bool compacted = ((tot64 >> 32) & 0x3FFFFFu) == 0u;
+        general = (tot64 >> 54) != 0u || total > PSS_FIN_LIST_CAP;
+        if (!general && !pss_list_finish_fast<NT>(a, row, c, sh.list, total, G, pre, sh.f, compacted)) {
             /* slow path: candidates below the row-wide bound may remain in the
              * list; they are below the K-th largest and never selected */
             pss_list_finish<NT>(a, row, c, sh.list, total, sh.f.g);
