@@ -1103,8 +1103,9 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_row_kernel(pss_args a, uint32_
  * (written by other workgroups of the same launch in the small-batch form). */
 #define PSS_SC1 16 /* buffer-load cache policy: device-scope coherent (sc1) */
 template <int NT>
-__device__ __forceinline__ void pss_fin_row(const pss_args& a, uint32_t row, uint32_t NS, pss_fin_shared& sh,
-                                            uint32_t* bits, uint32_t bit_words) {
+__device__ __forceinline__ void pss_fin_row(const pss_args& a, const sample_params* __restrict__ params,
+                                            uint32_t row, uint32_t NS, pss_fin_shared& sh, uint32_t* bits,
+                                            uint32_t bit_words) {
     static_assert(NT >= PSS_SEG_MAX_SLOTS, "one thread per item");
     static_assert(PSS_FIN_SPEC == 16u, "one 128-byte line per item");
     const uint32_t tid = pss_tid();
@@ -1129,15 +1130,21 @@ __device__ __forceinline__ void pss_fin_row(const pss_args& a, uint32_t row, uin
         v[2 * j] = ((unsigned long long)w.y << 32) | w.x;
         v[2 * j + 1] = ((unsigned long long)w.w << 32) | w.z;
     }
+    /* the row state in the same round trip (lane-varying zero offsets keep
+     * these loads vector loads, issued before anything is waited for); the
+     * parameters through scalar loads (`params` is never written here) */
     uint32_t z = 0u;
     __asm__ __volatile__("" : "+v"(z));
     const uint32_t G = pss_ld_agent(&ws->bound + z);
-    const uint32_t V = a.V;
-    const sample_params sp = a.params[row];
     pss_row_pre pre;
-    pre.rng = a.rng[row];
-    pre.step = a.step[row];
-    pre.pos = a.position[row];
+    pre.rng = a.rng[row + z];
+    pre.step = a.step[row + z];
+    pre.pos = a.position[row + z];
+    const uint32_t V = a.V;
+    const sample_params sp = params[row];
+    pre.rng = __builtin_amdgcn_readfirstlane(pre.rng);
+    pre.step = __builtin_amdgcn_readfirstlane(pre.step);
+    pre.pos = __builtin_amdgcn_readfirstlane(pre.pos);
     const bool greedy = (a.mode == PSS_MODE_GREEDY) || !(sp.temperature > 0.0f);
     const pss_rowcfg c = pss_make_rowcfg(sp, V);
 
@@ -1202,11 +1209,12 @@ __device__ __forceinline__ void pss_fin_row(const pss_args& a, uint32_t row, uin
 }
 
 /* One workgroup per row; NS items per row were written by pss_seg_kernel. */
-__global__ void __launch_bounds__(PSS_ST_NT) pss_fin_kernel(pss_args a, uint32_t NS) {
+__global__ void __launch_bounds__(PSS_ST_NT) pss_fin_kernel(pss_args a, uint32_t NS,
+                                                             const sample_params* __restrict__ params) {
     __shared__ pss_fin_shared sh;
     __shared__ uint32_t bits[PSS_MAX_VOCAB / 32];
     pss_globalize(a);
-    pss_fin_row<PSS_ST_NT>(a, blockIdx.x, NS, sh, bits, PSS_MAX_VOCAB / 32);
+    pss_fin_row<PSS_ST_NT>(a, params, blockIdx.x, NS, sh, bits, PSS_MAX_VOCAB / 32);
 }
 
 /*
@@ -1250,7 +1258,7 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_small_kernel(pss_args a, uint3
     }
     __syncthreads();
     if (!last) return;
-    pss_fin_row<PSS_SEG_NT>(a, row, NS, U.fin.fs, U.fin.bits, PSS_ROW_BITS);
+    pss_fin_row<PSS_SEG_NT>(a, params, row, NS, U.fin.fs, U.fin.bits, PSS_ROW_BITS);
 }
 
 /* ---------------------------------------------------------------------- */
@@ -1356,7 +1364,7 @@ static inline hipError_t pss_stream_go(const pss_args& a, uint32_t rows, uint32_
                : pss_seg_launch<EPT, PSS_DTYPE_F32, false>(a, NS, n_items, st);
     if (e != hipSuccess) return e;
     if (split_ev && (e = hipEventRecord(split_ev, st)) != hipSuccess) return e;
-    pss_fin_kernel<<<dim3(rows), dim3(PSS_ST_NT), 0, st>>>(a, NS);
+    pss_fin_kernel<<<dim3(rows), dim3(PSS_ST_NT), 0, st>>>(a, NS, a.params);
     return hipGetLastError();
 }
 
