@@ -30,41 +30,36 @@
 #define PSS_GEN_NT 1024
 #define PSS_NO_TOKEN 0xFFFFFFFFu
 
-/* Row-level epilogue (ArgMax-Reduce.comp:376-385 for sampled rows,
- * :161-165 for greedy rows).  Called by one thread. */
-__device__ __forceinline__ void pss_epilogue(const pss_args& a, uint32_t row, uint32_t tok, bool greedy,
-                                    uint32_t W, uint32_t new_rng, const pss_row_info& inf) {
-    a.result[row * PSS_RESULT_SLOTS + a.pass_idx] = tok;
-    a.token_ids[row] = tok;
-    uint32_t pos = a.position[row];
-    if (!greedy) {
-        if (W > 0u) a.history[row * PSS_MAX_PENALTY_LEN + pos % W] = tok;
-        if (a.rng_mode == PSS_RNG_PHILOX)
-            a.step[row] = a.step[row] + 1u;
-        else
-            a.rng[row] = new_rng;
-    }
-    if (a.do_inc) a.position[row] = pos + 1u;
-    if (a.host_tokens) a.host_tokens[row] = tok;
-    if (a.info) a.info[row] = inf;
+/* Output stores of the epilogue: write-through to memory (agent scope), so
+ * that the kernel's end has no dirty cache lines of them to write back
+ * (measured: a step ends ~0.3 us earlier than with plain stores). */
+__device__ __forceinline__ void pss_out(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* pss_epilogue with the row's position and Philox step already loaded. */
 __device__ __forceinline__ void pss_epilogue_pre(const pss_args& a, uint32_t row, uint32_t tok, bool greedy,
                                                  uint32_t W, uint32_t new_rng, const pss_row_info& inf,
                                                  uint32_t pos, uint32_t step) {
-    a.result[row * PSS_RESULT_SLOTS + a.pass_idx] = tok;
-    a.token_ids[row] = tok;
+    pss_out(&a.result[row * PSS_RESULT_SLOTS + a.pass_idx], tok);
+    pss_out(&a.token_ids[row], tok);
     if (!greedy) {
-        if (W > 0u) a.history[row * PSS_MAX_PENALTY_LEN + pos % W] = tok;
+        if (W > 0u) pss_out(&a.history[row * PSS_MAX_PENALTY_LEN + pos % W], tok);
         if (a.rng_mode == PSS_RNG_PHILOX)
-            a.step[row] = step + 1u;
+            pss_out(&a.step[row], step + 1u);
         else
-            a.rng[row] = new_rng;
+            pss_out(&a.rng[row], new_rng);
     }
-    if (a.do_inc) a.position[row] = pos + 1u;
+    if (a.do_inc) pss_out(&a.position[row], pos + 1u);
     if (a.host_tokens) a.host_tokens[row] = tok;
     if (a.info) a.info[row] = inf;
+}
+
+/* Row-level epilogue (ArgMax-Reduce.comp:376-385 for sampled rows,
+ * :161-165 for greedy rows).  Called by one thread. */
+__device__ __forceinline__ void pss_epilogue(const pss_args& a, uint32_t row, uint32_t tok, bool greedy,
+                                             uint32_t W, uint32_t new_rng, const pss_row_info& inf) {
+    pss_epilogue_pre(a, row, tok, greedy, W, new_rng, inf, a.position[row], a.step[row]);
 }
 
 /* Uniform of the draw from the row's rng state s and Philox step, and the

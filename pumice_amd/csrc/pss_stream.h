@@ -97,7 +97,7 @@ struct pss_row_lds {
 struct pss_fin_small {
     unsigned long long cl[PSS_FAST_N]; /* fast path: entries at or above the row bound */
     unsigned long long kept[64];       /* fast path: entries at or above the K-th largest */
-    uint32_t hist[256];                /* fast path: radix digit counts */
+    uint32_t hist[2][256];             /* fast path: radix digit counts (alternate passes) */
     pss_gen_shared g;
     uint32_t mx[PSS_SEG_NW];           /* per-wave largest key */
     uint32_t digit;
@@ -350,9 +350,14 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
             k[r] = i < nc ? (uint32_t)(e[r] >> 32) : 0u;
             kmax = k[r] > kmax ? k[r] : kmax;
         }
-        kmax = wave_max_u32(kmax);
-        if (lane == 0) sh.mx[wave] = kmax;
-        __syncthreads();
+        if (!compacted) {
+            /* (the gathering caller published the per-wave maxima and
+             * cleared both histograms before its barrier) */
+            kmax = wave_max_u32(kmax);
+            if (lane == 0) sh.mx[wave] = kmax;
+            if (tid < 256u) sh.hist[0][tid] = sh.hist[1][tid] = 0u;
+            __syncthreads();
+        }
         uint32_t tmaxKey = 0;
 #pragma unroll
         for (int w = 0; w < NT / PSS_WAVE; ++w) tmaxKey = sh.mx[w] > tmaxKey ? sh.mx[w] : tmaxKey;
@@ -364,15 +369,17 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
             uint32_t pmask = shift + 8 >= 32 ? 0u : ~((1u << (shift + 8)) - 1u);
             uint32_t prefix = tmaxKey & pmask;
             uint32_t rem = c.K, nab = 0u;
-            for (; shift >= 0; shift -= 8) {
-                if (tid < 256u) sh.hist[tid] = 0u;
-                __syncthreads();
+            for (int pass = 0; shift >= 0; shift -= 8, ++pass) {
+                /* histogram pass & 1; the other one (read two barriers
+                 * ago) is cleared for the next pass meanwhile */
+                uint32_t* hist = sh.hist[pass & 1];
+                if (pass > 0 && tid < 256u) sh.hist[(pass + 1) & 1][tid] = 0u;
 #pragma unroll
                 for (int r = 0; r < R; ++r)
-                    if (k[r] && (k[r] & pmask) == prefix) atomicAdd(&sh.hist[(k[r] >> shift) & 255u], 1u);
+                    if (k[r] && (k[r] & pmask) == prefix) atomicAdd(&hist[(k[r] >> shift) & 255u], 1u);
                 __syncthreads();
                 if (tid < 64) {
-                    const uint4 h = *(const uint4*)&sh.hist[4u * lane];
+                    const uint4 h = *(const uint4*)&hist[4u * lane];
                     const uint32_t s4 = h.x + h.y + h.z + h.w;
                     const uint32_t above = (uint32_t)(wave_incl_suffix_u64(s4) - s4); /* lanes > lane */
                     if (above < rem && rem <= above + s4) {
@@ -410,11 +417,17 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
             tauK = prefix;
         }
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (k[r] && k[r] >= tauK) {
-                const uint32_t pos = atomicAdd(&sh.nk, 1u);
-                if (pos < 64u) sh.kept[pos] = e[r];
+        for (int r = 0; r < R; ++r) {
+            const bool kp = k[r] && k[r] >= tauK;
+            const uint64_t m = __ballot(kp);
+            if (m) {
+                uint32_t b0 = 0u;
+                if (lane == 0u) b0 = atomicAdd(&sh.nk, (uint32_t)__popcll(m));
+                const uint32_t pos = __builtin_amdgcn_readfirstlane(b0) +
+                                     __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+                if (kp && pos < 64u) sh.kept[pos] = e[r];
             }
+        }
         __syncthreads();
         cnt = sh.nk;
         if (cnt > 64u) return false;
@@ -1096,14 +1109,28 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_row_kernel(pss_args a, uint32_
  * is requested in one round trip before anything is waited for: thread s < NS
  * loads item s's count, its greedy best and the first PSS_FIN_SPEC entries
  * of its pool range (one 128-byte line; an item rarely has more, the rest
- * follow in a second trip), every thread the row-wide bound G, together with
- * the row's parameters and state.  Of the first PSS_FIN_SPEC entries only
+ * follow in a second trip), every thread the row-wide bound G; the row's
+ * parameters and state come loaded by the caller.  Of the first PSS_FIN_SPEC
+ * entries only
  * those at or above G are gathered; when no item had more, the list is
  * already compacted for the finisher.  Workspace reads are agent-scope
  * (written by other workgroups of the same launch in the small-batch form). */
 #define PSS_SC1 16 /* buffer-load cache policy: device-scope coherent (sc1) */
+
+/* The row's parameters (scalar loads: `params` is never written by these
+ * kernels) and state (vector loads through a lane-varying zero offset, so
+ * that issuing them waits for nothing; pss_fin_row makes them uniform). */
+__device__ __forceinline__ void pss_load_row_state(const pss_args& a, const sample_params* __restrict__ params,
+                                                   uint32_t row, sample_params& sp, pss_row_pre& pre) {
+    uint32_t z = 0u;
+    __asm__ __volatile__("" : "+v"(z));
+    pre.rng = a.rng[row + z];
+    pre.step = a.step[row + z];
+    pre.pos = a.position[row + z];
+    sp = params[row];
+}
 template <int NT>
-__device__ __forceinline__ void pss_fin_row(const pss_args& a, const sample_params* __restrict__ params,
+__device__ __forceinline__ void pss_fin_row(const pss_args& a, const sample_params& sp, const pss_row_pre& pre_in,
                                             uint32_t row, uint32_t NS, pss_fin_shared& sh, uint32_t* bits,
                                             uint32_t bit_words) {
     static_assert(NT >= PSS_SEG_MAX_SLOTS, "one thread per item");
@@ -1130,21 +1157,14 @@ __device__ __forceinline__ void pss_fin_row(const pss_args& a, const sample_para
         v[2 * j] = ((unsigned long long)w.y << 32) | w.x;
         v[2 * j + 1] = ((unsigned long long)w.w << 32) | w.z;
     }
-    /* the row state in the same round trip (lane-varying zero offsets keep
-     * these loads vector loads, issued before anything is waited for); the
-     * parameters through scalar loads (`params` is never written here) */
     uint32_t z = 0u;
     __asm__ __volatile__("" : "+v"(z));
     const uint32_t G = pss_ld_agent(&ws->bound + z);
     pss_row_pre pre;
-    pre.rng = a.rng[row + z];
-    pre.step = a.step[row + z];
-    pre.pos = a.position[row + z];
+    pre.rng = __builtin_amdgcn_readfirstlane(pre_in.rng);
+    pre.step = __builtin_amdgcn_readfirstlane(pre_in.step);
+    pre.pos = __builtin_amdgcn_readfirstlane(pre_in.pos);
     const uint32_t V = a.V;
-    const sample_params sp = params[row];
-    pre.rng = __builtin_amdgcn_readfirstlane(pre.rng);
-    pre.step = __builtin_amdgcn_readfirstlane(pre.step);
-    pre.pos = __builtin_amdgcn_readfirstlane(pre.pos);
     const bool greedy = (a.mode == PSS_MODE_GREEDY) || !(sp.temperature > 0.0f);
     const pss_rowcfg c = pss_make_rowcfg(sp, V);
 
@@ -1192,6 +1212,15 @@ __device__ __forceinline__ void pss_fin_row(const pss_args& a, const sample_para
                     if (i0 + u < n0) sh.list[o++] = w[u];
             }
         }
+        /* for the finisher: per-wave largest gathered key, cleared radix
+         * histograms (both before the barrier) */
+        uint32_t mk = 0u;
+#pragma unroll
+        for (uint32_t u = 0; u < PSS_FIN_SPEC; ++u)
+            mk = ((keep >> u) & 1u) && (uint32_t)(v[u] >> 32) > mk ? (uint32_t)(v[u] >> 32) : mk;
+        mk = wave_max_u32(mk);
+        if ((tid & 63u) == 0u) sh.f.mx[tid >> 6] = mk;
+        if (tid < 256u) sh.f.hist[0][tid] = sh.f.hist[1][tid] = 0u;
         if (tid == 0) sh.f.gtot = tot64;
         __syncthreads();
         tot64 = sh.f.gtot;
@@ -1214,7 +1243,10 @@ __global__ void __launch_bounds__(PSS_ST_NT) pss_fin_kernel(pss_args a, uint32_t
     __shared__ pss_fin_shared sh;
     __shared__ uint32_t bits[PSS_MAX_VOCAB / 32];
     pss_globalize(a);
-    pss_fin_row<PSS_ST_NT>(a, params, blockIdx.x, NS, sh, bits, PSS_MAX_VOCAB / 32);
+    sample_params sp;
+    pss_row_pre pre;
+    pss_load_row_state(a, params, blockIdx.x, sp, pre);
+    pss_fin_row<PSS_ST_NT>(a, sp, pre, blockIdx.x, NS, sh, bits, PSS_MAX_VOCAB / 32);
 }
 
 /*
@@ -1247,6 +1279,10 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_small_kernel(pss_args a, uint3
     const uint32_t row = blockIdx.x / GW, g = blockIdx.x - row * GW;
     const uint32_t s0 = g * NS / GW, s1 = (g + 1u) * NS / GW;
     const uint32_t tid = pss_tid();
+    /* the finisher's row state, off its critical path (every workgroup) */
+    sample_params sp;
+    pss_row_pre pre;
+    pss_load_row_state(a, params, row, sp, pre);
     pss_seg_rounds<EPT, DT, M1, false, true>(a, NS, row * NS + s0, row * NS + s1, params, U.st, joint, nullptr);
     pss_wait_mem(); /* this wave's pool stores, counts and staged loads have completed */
     __syncthreads();
@@ -1258,7 +1294,7 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_small_kernel(pss_args a, uint3
     }
     __syncthreads();
     if (!last) return;
-    pss_fin_row<PSS_SEG_NT>(a, params, row, NS, U.fin.fs, U.fin.bits, PSS_ROW_BITS);
+    pss_fin_row<PSS_SEG_NT>(a, sp, pre, row, NS, U.fin.fs, U.fin.bits, PSS_ROW_BITS);
 }
 
 /* ---------------------------------------------------------------------- */
