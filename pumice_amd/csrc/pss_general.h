@@ -30,12 +30,10 @@
 #define PSS_GEN_NT 1024
 #define PSS_NO_TOKEN 0xFFFFFFFFu
 
-/* Output stores of the epilogue: write-through to memory (agent scope), so
- * that the kernel's end has no dirty cache lines of them to write back
- * (measured: a step ends ~0.3 us earlier than with plain stores). */
-__device__ __forceinline__ void pss_out(uint32_t* p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+/* Output stores of the epilogue: plain stores.  (Write-through agent-scope
+ * stores end a headline step ~0.3 us earlier but slow the 256-id-window fp16
+ * workload by ~10 us per step, so they are not used.) */
+__device__ __forceinline__ void pss_out(uint32_t* p, uint32_t v) { *p = v; }
 
 /* pss_epilogue with the row's position and Philox step already loaded. */
 __device__ __forceinline__ void pss_epilogue_pre(const pss_args& a, uint32_t row, uint32_t tok, bool greedy,

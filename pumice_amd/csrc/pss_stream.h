@@ -42,7 +42,8 @@
 #define PSS_SEG_MAX_SLOTS 256u   /* items per row (V <= 262144 at items >= 1024 ids) */
 #define PSS_POOL_CAP 16384u      /* pool entries per row, split evenly over its items */
 #define PSS_FIN_LIST_CAP 4096u   /* candidates the finisher gathers in LDS */
-#define PSS_FAST_N 1024u         /* candidates the fast finisher handles (K <= 64) */
+#define PSS_FAST_N 1024u         /* candidates the fast finisher handles (K <= PSS_SEG_KMAX) */
+#define PSS_KEPT_CAP 256u        /* entries at or above the K-th largest the fast finisher handles */
 #define PSS_SEG_OVERFLOW 0xFFFFFFFFu
 #define PSS_KEY_NEG_INF 0x007FFFFFu /* pss_key(-inf): the smallest key of any element */
 
@@ -96,7 +97,7 @@ struct pss_row_lds {
 /* Finisher scratch besides the candidate list. */
 struct pss_fin_small {
     unsigned long long cl[PSS_FAST_N]; /* fast path: entries at or above the row bound */
-    unsigned long long kept[64];       /* fast path: entries at or above the K-th largest */
+    unsigned long long kept[PSS_KEPT_CAP]; /* fast path: entries at or above the K-th largest */
     uint32_t hist[2][256];             /* fast path: radix digit counts (alternate passes) */
     pss_gen_shared g;
     uint32_t mx[PSS_SEG_NW];           /* per-wave largest key */
@@ -119,13 +120,18 @@ struct pss_fin_shared {
  * Select by cumulative weight from the top over the list: kw(e, key, w) gives
  * entry e's selection key and weight (w = 0 skips it).  Returns the largest
  * key v with sum_{key >= v} w >= rem (1 <= rem <= total weight).  Digits of 8
- * bits from bit top_shift + 7 down; 256-bin LDS histograms.
+ * bits from bit top_shift + 7 down; 256-bin LDS histograms.  Every weighted
+ * key shares its bits above top_shift + 7 with `above` (the callers start
+ * below the common prefix of a lower bound and the maximum, so the first
+ * digit spreads over bins instead of piling onto one).
  */
 template <int NT, class KW>
 __device__ __forceinline__ uint32_t pss_list_select(pss_gen_shared& sh, const unsigned long long* list,
-                                                    uint32_t n, uint64_t rem, int top_shift, KW kw) {
+                                                    uint32_t n, uint64_t rem, int top_shift, uint32_t above,
+                                                    KW kw) {
     const uint32_t tid = threadIdx.x;
-    uint32_t prefix = 0, pmask = 0;
+    uint32_t pmask = top_shift + 8 >= 32 ? 0u : ~((1u << (top_shift + 8)) - 1u);
+    uint32_t prefix = above & pmask;
     for (int shift = top_shift; shift >= 0; shift -= 8) {
         for (uint32_t i = tid; i < 256u; i += NT) sh.hist[i] = 0;
         __syncthreads();
@@ -147,12 +153,21 @@ __device__ __forceinline__ uint32_t pss_list_select(pss_gen_shared& sh, const un
     return prefix;
 }
 
+/* First digit shift for a select between lower bound lo and maximum hi
+ * (lo <= hi): below their common prefix; -1 when they are equal. */
+__device__ __forceinline__ int pss_select_shift(uint32_t lo, uint32_t hi) {
+    const uint32_t d = lo ^ hi;
+    return d ? ((31 - (int)__clz(d)) / 8) * 8 : -1;
+}
+
 /* Finish a sampled row from n candidates (LDS) that contain every element at
- * or above the row's K-th largest value.  Any K, any number of ties. */
+ * or above the row's K-th largest value; G is a lower bound on that value
+ * with at least K candidates at or above it (0: none known).  Any K, any
+ * number of ties. */
 template <int NT>
 __device__ __forceinline__ void pss_list_finish(const pss_args& a, uint32_t row, const pss_rowcfg& c,
                                                 const unsigned long long* list, uint32_t n,
-                                                pss_gen_shared& sh) {
+                                                pss_gen_shared& sh, uint32_t G) {
     const uint32_t tid = threadIdx.x;
     uint64_t mk = 0;
     for (uint32_t i = tid; i < n; i += NT) {
@@ -162,12 +177,15 @@ __device__ __forceinline__ void pss_list_finish(const pss_args& a, uint32_t row,
     const uint32_t tmaxKey = (uint32_t)block_max_u64<NT>(mk, sh.red);
     const float tmax = pss_unkey(tmaxKey);
 
-    /* S5: exact K-th largest */
-    const uint32_t tauK = pss_list_select<NT>(sh, list, n, c.K, 24,
-                                              [&](unsigned long long e, uint32_t& k, uint64_t& w) {
-                                                  k = (uint32_t)(e >> 32);
-                                                  w = 1u;
-                                              });
+    /* S5: exact K-th largest, over the candidates at or above G */
+    const uint32_t g = G <= tmaxKey ? G : 0u;
+    const int shK = pss_select_shift(g, tmaxKey);
+    const uint32_t tauK = shK < 0 ? tmaxKey
+                                  : pss_list_select<NT>(sh, list, n, c.K, shK, tmaxKey,
+                                                        [&](unsigned long long e, uint32_t& k, uint64_t& w) {
+                                                            k = (uint32_t)(e >> 32);
+                                                            w = k >= g ? 1u : 0u;
+                                                        });
     auto qof = [&](uint32_t k) -> uint64_t { return pss_fixq(pss_prob(pss_unkey(k), tmax)); };
     uint64_t zl = 0;
     for (uint32_t i = tid; i < n; i += NT) {
@@ -180,11 +198,13 @@ __device__ __forceinline__ void pss_list_finish(const pss_args& a, uint32_t row,
     uint32_t tau = tauK;
     if (c.useTopP) {
         const uint64_t need = pss_topp_need(c.topP, zk);
-        const uint32_t tauP = pss_list_select<NT>(sh, list, n, need, 24,
-                                                  [&](unsigned long long e, uint32_t& k, uint64_t& w) {
-                                                      k = (uint32_t)(e >> 32);
-                                                      w = k >= tauK ? qof(k) : 0u;
-                                                  });
+        const int shP = pss_select_shift(tauK, tmaxKey);
+        const uint32_t tauP = shP < 0 ? tmaxKey
+                                      : pss_list_select<NT>(sh, list, n, need, shP, tmaxKey,
+                                                            [&](unsigned long long e, uint32_t& k, uint64_t& w) {
+                                                                k = (uint32_t)(e >> 32);
+                                                                w = k >= tauK ? qof(k) : 0u;
+                                                            });
         tau = tauP > tau ? tauP : tau;
     }
 
@@ -220,7 +240,7 @@ __device__ __forceinline__ void pss_list_finish(const pss_args& a, uint32_t row,
     const uint64_t target = pss_draw_target(u24, Z);
     uint32_t tok, flags = 0;
     if (Z > 0) {
-        tok = pss_list_select<NT>(sh, list, n, Z - target, 16,
+        tok = pss_list_select<NT>(sh, list, n, Z - target, 16, 0u,
                                   [&](unsigned long long e, uint32_t& k, uint64_t& w) {
                                       float p;
                                       k = (uint32_t)e;
@@ -274,7 +294,144 @@ struct pss_row_pre {
 };
 
 /*
- * Fast finisher for K <= 64 and up to PSS_FAST_N candidates (list), those
+ * One wave, no barriers: the largest key v with sum_{key >= v} w >= rem
+ * (1 <= rem <= total weight) over the R (key, weight) pairs of each lane.
+ * Digits of 8 bits from bit top_shift + 7 down, every weighted key sharing
+ * its bits above that with `above`; the histogram is 256 u64 of LDS the wave
+ * owns (a wave's LDS operations complete in order, so no wait is needed
+ * between clearing, adding and reading).
+ */
+template <int R>
+__device__ __forceinline__ uint32_t pss_wave_wselect(const uint32_t (&k)[R], const uint64_t (&w)[R], uint64_t rem,
+                                                     int top_shift, uint32_t above, uint64_t* hist) {
+    const uint32_t lane = pss_tid() & 63u;
+    uint32_t pmask = top_shift + 8 >= 32 ? 0u : ~((1u << (top_shift + 8)) - 1u);
+    uint32_t prefix = above & pmask;
+    for (int shift = top_shift; shift >= 0; shift -= 8) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) hist[4u * lane + (uint32_t)i] = 0ull;
+        __asm__ __volatile__("" ::: "memory");
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (w[r] && (k[r] & pmask) == prefix)
+                atomicAdd((unsigned long long*)&hist[(k[r] >> shift) & 255u], (unsigned long long)w[r]);
+        __asm__ __volatile__("" ::: "memory");
+        const uint64_t h[4] = {hist[4u * lane], hist[4u * lane + 1u], hist[4u * lane + 2u], hist[4u * lane + 3u]};
+        const uint64_t s4 = h[0] + h[1] + h[2] + h[3];
+        const uint64_t incl = wave_incl_suffix_u64(s4); /* lanes >= lane */
+        const uint64_t abv = incl - s4;                  /* lanes > lane */
+        const bool hit = abv < rem && rem <= incl;
+        uint32_t dg = 0u;
+        uint64_t cum = abv;
+        if (hit) {
+            dg = 4u * lane;
+            for (int i = 3; i >= 0; --i) {
+                if (cum + h[i] >= rem) {
+                    dg = 4u * lane + (uint32_t)i;
+                    break;
+                }
+                cum += h[i];
+            }
+        }
+        const uint32_t src = (uint32_t)__ffsll((long long)__ballot(hit)) - 1u;
+        prefix |= wave_read_u32(dg, src) << shift;
+        pmask |= 0xFFu << shift;
+        rem -= wave_read_u64(cum, src);
+    }
+    return prefix;
+}
+
+/*
+ * Finisher tail for 65..256 entries (src) at or above the exact K-th largest
+ * key tauK (maximum tmaxKey), run by wave 0 alone, four entries per lane:
+ * masses, the top-p cut as a weighted select over keys (the largest key whose
+ * mass at or above it reaches the need: the same cut as a scan in key
+ * order), min-p, and the draw as a weighted select over ids (the largest id
+ * v whose kept mass at or above it reaches Z - target is the first id, in
+ * ascending order, whose cumulative mass exceeds the target).
+ */
+__device__ __forceinline__ void pss_wave_tail4(const pss_args& a, uint32_t row, const pss_rowcfg& c,
+                                            const unsigned long long* src, uint32_t cnt, uint32_t tauK,
+                                            uint32_t tmaxKey, const pss_row_pre& pre, uint32_t u24,
+                                            uint32_t newRng, uint64_t* hist) {
+    const uint32_t lane = pss_tid() & 63u;
+    const float tmax = pss_unkey(tmaxKey);
+    uint32_t key[4], id[4];
+    float p[4];
+    uint64_t q[4];
+    bool v[4];
+    uint64_t qs = 0u;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t i = lane + 64u * (uint32_t)r;
+        v[r] = i < cnt;
+        const unsigned long long e = v[r] ? src[i] : 0ull;
+        key[r] = (uint32_t)(e >> 32);
+        id[r] = (uint32_t)e;
+        p[r] = v[r] ? pss_prob(pss_unkey(key[r]), tmax) : 0.0f;
+        q[r] = v[r] ? pss_fixq(p[r]) : 0ull;
+        qs += q[r];
+    }
+    const uint64_t zk = wave_sum_u64(qs);
+    uint32_t tau = tauK;
+    if (c.useTopP) {
+        const uint64_t need = pss_topp_need(c.topP, zk);
+        const int sh = pss_select_shift(tauK, tmaxKey);
+        const uint32_t tauP = sh < 0 ? tmaxKey : pss_wave_wselect<4>(key, q, need, sh, tmaxKey, hist);
+        tau = tauP > tau ? tauP : tau;
+    }
+    uint64_t kq[4];
+    bool kp[4];
+    uint64_t zs = 0u;
+    uint32_t kc = 0u, last = 0u;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        kp[r] = v[r] && key[r] >= tau && (!c.useMinP || p[r] >= c.minP);
+        kq[r] = kp[r] ? q[r] : 0ull;
+        zs += kq[r];
+        kc += (uint32_t)__popcll(__ballot(kp[r]));
+        last = kp[r] && id[r] + 1u > last ? id[r] + 1u : last;
+    }
+    const uint64_t Z = wave_sum_u64(zs);
+    const uint32_t lastAll = wave_max_u32(last);
+    const uint64_t target = pss_draw_target(u24, Z);
+    uint32_t tok, flags = 0;
+    if (Z > 0) {
+        tok = pss_wave_wselect<4>(id, kq, Z - target, 16, 0u, hist);
+    } else {
+        tok = lastAll > 0u ? lastAll - 1u : 0u;
+        flags |= PSS_INFO_FALLBACK;
+    }
+    if (a.kept_mask || a.probs) {
+        if (a.kept_mask)
+            for (uint32_t w = lane; w < a.mask_words; w += 64u) a.kept_mask[(size_t)row * a.mask_words + w] = 0u;
+        if (a.probs)
+            for (uint32_t j = lane; j < a.V; j += 64u) a.probs[(size_t)row * a.probs_stride + j] = 0.0f;
+        pss_wait_mem();
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (kp[r]) {
+                if (a.kept_mask) atomicOr(&a.kept_mask[(size_t)row * a.mask_words + (id[r] >> 5)], 1u << (id[r] & 31u));
+                if (a.probs) a.probs[(size_t)row * a.probs_stride + id[r]] = p[r] / ((float)Z * 0x1.0p-45f);
+            }
+    }
+    if (lane == 0) {
+        pss_row_info inf = {};
+        inf.token = tok;
+        inf.kept_count = kc;
+        inf.tau_key = tau;
+        inf.tmax_key = tmaxKey;
+        inf.z_kept = Z;
+        inf.z_topk = zk;
+        inf.target = target;
+        inf.u24 = u24;
+        inf.flags = flags;
+        pss_epilogue_pre(a, row, tok, false, c.W, newRng, inf, pre.pos, pre.step);
+    }
+}
+
+/*
+ * Fast finisher for up to PSS_FAST_N candidates (list), those
  * below the row-wide bound G ignored (G is at most the K-th largest value,
  * so every entry of the top-K is at or above it):
  *   1. the entries at or above G are compacted into sh.cl (unless the
@@ -293,8 +450,11 @@ struct pss_row_pre {
  *      the owning lanes, scan, take the first id whose cumulative mass
  *      exceeds the draw target.  Lane exchanges are DPP / permlane /
  *      bpermute.
- * Returns false (nothing written) when more than 64 entries are at or above
- * the K-th largest (heavy ties).
+ * With 65..PSS_KEPT_CAP entries at or above the exact K-th largest (K > 64,
+ * or ties), wave 0 finishes with pss_wave_tail4 instead of step 3.  Returns
+ * false (nothing written) for K > PSS_SEG_KMAX, more than PSS_FAST_N
+ * candidates, or more than PSS_KEPT_CAP entries at or above the K-th largest
+ * (heavy ties).
  */
 template <int NT>
 __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t row,
@@ -303,7 +463,7 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
                                                      pss_fin_small& sh, bool compacted = false) {
     constexpr int R = (int)((PSS_FAST_N + NT - 1) / NT);
     static_assert(NT >= 256 && NT <= 1024, "radix bins: the first 256 threads");
-    if (c.K > 64u || n > PSS_FAST_N) return false;
+    if (c.K > PSS_SEG_KMAX || n > PSS_FAST_N) return false;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     /* the draw depends on the row state only: off the serial tail */
     uint32_t newRng;
@@ -425,13 +585,19 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
                 if (lane == 0u) b0 = atomicAdd(&sh.nk, (uint32_t)__popcll(m));
                 const uint32_t pos = __builtin_amdgcn_readfirstlane(b0) +
                                      __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-                if (kp && pos < 64u) sh.kept[pos] = e[r];
+                if (kp && pos < PSS_KEPT_CAP) sh.kept[pos] = e[r];
             }
         }
         __syncthreads();
         cnt = sh.nk;
-        if (cnt > 64u) return false;
+        if (cnt > PSS_KEPT_CAP) return false;
         src = sh.kept;
+        if (cnt > 64u) {
+            /* 65..256 entries at or above the exact K-th largest: wave 0,
+             * four per lane, weighted selects instead of sorts */
+            if (tid < 64) pss_wave_tail4(a, row, c, sh.kept, cnt, tauK, tmaxKey, pre, u24, newRng, sh.g.hist);
+            return true;
+        }
     }
     if (cnt == 0u) return false;
 
@@ -1096,7 +1262,7 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_row_kernel(pss_args a, uint32_
     const uint32_t n = rl.n;
     bool general = !covered || n > PSS_ROW_LIST_CAP;
     if (!general && !pss_list_finish_fast<NT>(a, row, c, rl.list, n, rl.bound, pre, U.fin.f))
-        pss_list_finish<NT>(a, row, c, rl.list, n, U.fin.f.g);
+        pss_list_finish<NT>(a, row, c, rl.list, n, U.fin.f.g, rl.bound);
     if (general) pss_general_row<NT>(a, row, U.fin.f.g, U.fin.bits, PSS_ROW_BITS);
 }
 
@@ -1230,7 +1396,7 @@ __device__ __forceinline__ void pss_fin_row(const pss_args& a, const sample_para
         if (!general && !pss_list_finish_fast<NT>(a, row, c, sh.list, total, G, pre, sh.f, compacted)) {
             /* slow path: candidates below the row-wide bound may remain in the
              * list; they are below the K-th largest and never selected */
-            pss_list_finish<NT>(a, row, c, sh.list, total, sh.f.g);
+            pss_list_finish<NT>(a, row, c, sh.list, total, sh.f.g, G);
         }
         if (tid == 0) pss_st_agent(&ws->bound, 0u); /* for the next launch */
     }
@@ -1279,10 +1445,6 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_small_kernel(pss_args a, uint3
     const uint32_t row = blockIdx.x / GW, g = blockIdx.x - row * GW;
     const uint32_t s0 = g * NS / GW, s1 = (g + 1u) * NS / GW;
     const uint32_t tid = pss_tid();
-    /* the finisher's row state, off its critical path (every workgroup) */
-    sample_params sp;
-    pss_row_pre pre;
-    pss_load_row_state(a, params, row, sp, pre);
     pss_seg_rounds<EPT, DT, M1, false, true>(a, NS, row * NS + s0, row * NS + s1, params, U.st, joint, nullptr);
     pss_wait_mem(); /* this wave's pool stores, counts and staged loads have completed */
     __syncthreads();
@@ -1294,6 +1456,9 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_small_kernel(pss_args a, uint3
     }
     __syncthreads();
     if (!last) return;
+    sample_params sp;
+    pss_row_pre pre;
+    pss_load_row_state(a, params, row, sp, pre);
     pss_fin_row<PSS_SEG_NT>(a, sp, pre, row, NS, U.fin.fs, U.fin.bits, PSS_ROW_BITS);
 }
 
