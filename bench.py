@@ -10,9 +10,10 @@ A "step" is one pss_enqueue over a batch of logit rows resident in HBM.
             working set (>= 600 MB) exceeds the 256 MB last-level cache and
             rows come from HBM.  One step is one launch of pss_row_kernel (or, with
             --split / --general, the other two forms).
-  latency   batch 1 (config c2): launch-to-token p50/p90 (host clock, token
-            stored by the kernel into pinned host memory), per-step GPU time,
-            and steady decode-group us/token through the C generate loop.
+  latency   batch 1 (config c2; the small-batch form, pss_small_kernel):
+            launch-to-token p50/p90 (host clock, token stored by the kernel
+            into pinned host memory), per-step GPU time, and steady
+            decode-group us/token through the C generate loop.
   c3/c4/c5  the other batched configurations, rows/s and GB/s.
   cpu_baseline  the O1 oracle (scalar C, sort-based) on the box's host cores
             over a bounded sample of the headline rows.
@@ -77,14 +78,20 @@ def bench_batched(w, steps, warmup, flags=0):
     for i in range(warmup):
         s.enqueue(bufs[i % NBUF].ptr, dtype, w.V, w.rows, flags=flags)
     hip.stream_sync(stream)
-    # timed region: exactly `steps` launches, synchronized on both sides
+    # timed region: exactly `steps` launches, synchronized on both sides, and
+    # bracketed by HIP events on the sampler's stream (GPU time per launch,
+    # back to back)
+    ev0, ev1 = hip.Event(), hip.Event()
     hip.synchronize()
     t0 = time.perf_counter()
+    ev0.record(stream)
     for i in range(steps):
         s.enqueue(bufs[i % NBUF].ptr, dtype, w.V, w.rows, flags=flags)
+    ev1.record(stream)
     hip.stream_sync(stream)
     hip.synchronize()
     wall = time.perf_counter() - t0
+    stream_ms = ev0.elapsed_ms(ev1) / steps
     # per-launch GPU time with HIP events on the sampler's stream around each
     # launch (and, split form, the event between its two kernels)
     n_ev = min(steps, 100)
@@ -104,8 +111,10 @@ def bench_batched(w, steps, warmup, flags=0):
     bpr = w.bytes_per_row()
     k_ms = float(np.mean(kt))
     out = dict(rows=w.rows, V=w.V, dtype=str(w.logits.dtype), ms_per_step=wall * 1e3 / steps,
-               rows_per_s=w.rows * steps / wall, launch_ms_mean=k_ms, launch_ms_p50=pct(kt, 50),
+               rows_per_s=w.rows * steps / wall, stream_ms_per_launch=stream_ms,
+               launch_ms_mean=k_ms, launch_ms_p50=pct(kt, 50),
                bytes_per_row=bpr, bytes_per_launch=bpr * w.rows,
+               stream_gbps=bpr * w.rows / (stream_ms * 1e-3) / 1e9,
                launch_gbps=bpr * w.rows / (k_ms * 1e-3) / 1e9,
                wall_gbps=bpr * w.rows * steps / wall / 1e9)
     if split:
@@ -141,6 +150,15 @@ def bench_latency(steps):
         ev[i][1].record(stream)
     hip.stream_sync(stream)
     gpu_us = [a.elapsed_ms(b) * 1e3 for a, b in ev]
+    # back-to-back steps (a decode loop whose next step is already queued):
+    # events bracketing n_ev launches
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(stream)
+    for i in range(n_ev):
+        s.enqueue(dev[i % nrows].ptr, S.DTYPE_F32, w.V, 1, rng_mode=S.RNG_PHILOX)
+    e1.record(stream)
+    hip.stream_sync(stream)
+    b2b_us = e0.elapsed_ms(e1) * 1e3 / n_ev
     # steady decode groups through the C generate loop
     toks_gen, r = G.generate(s, table, steps, rows=1, rng_mode=S.RNG_PHILOX)
     s.close()
@@ -148,7 +166,7 @@ def bench_latency(steps):
     for d in dev:
         d.free()
     return dict(steps=steps, launch_to_token_us_p50=pct(lat, 50), launch_to_token_us_p90=pct(lat, 90),
-                gpu_us_p50=pct(gpu_us, 50), gpu_us_p90=pct(gpu_us, 90),
+                gpu_us_p50=pct(gpu_us, 50), gpu_us_p90=pct(gpu_us, 90), back_to_back_us_per_step=b2b_us,
                 decode_group_us_per_token=r["wall_us"] / max(r["emitted"], 1))
 
 
@@ -265,6 +283,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline only (c3/c4/c5 and latency skipped)")
+    ap.add_argument("--latency-only", action="store_true",
+                    help="only the batch-1 latency section (for kernel traces of the small-batch form)")
     ap.add_argument("--general", action="store_true", help="force the general kernel")
     ap.add_argument("--split", action="store_true", help="force the two-kernel form")
     ap.add_argument("--copy-calib", action="store_true",
@@ -285,6 +305,11 @@ def main():
     from pumice_amd import sampler as S
     from pumice_amd import workloads as WL
 
+    if args.latency_only:
+        log("latency (batch 1)")
+        lat = bench_latency(args.latency_steps)
+        print(json.dumps({"latency_b1": lat}), flush=True)
+        return
     flags = S.ENQ_GENERAL if args.general else (S.ENQ_SPLIT if args.split else 0)
     kernel = "general" if args.general else ("split" if args.split else "fused")
     log("generating headline workload")
@@ -322,8 +347,10 @@ def main():
         if kernel != "fused":
             traffic = None
     # dominant (fused: only) kernel: algorithmic bytes per launch / mean
-    # per-launch time from HIP events on the sampler's stream
-    achieved = h["launch_gbps"]
+    # per-launch time from HIP events on the sampler's stream bracketing the
+    # timed back-to-back launches (events around single launches, which add
+    # the dispatch, are in headline.launch_ms_*)
+    achieved = h["stream_gbps"]
     line = {
         "metric": "sampled rows/sec + HBM GB/s at V=102,400 (B=256); p50 µs/token at B=1",
         "value": h["rows_per_s"],
@@ -340,7 +367,7 @@ def main():
         "config": {
             "workload": "headline: 256 rows x V=102,400 fp32 logits, rep 1.1 + presence 0.5 over a "
                         "64-id window, T 0.8, top-k 40, top-p 0.95, min-p 0.05, xorshift32 seeds 0..255",
-            "rows": 256, "vocab": 102400, "kernel": kernel,
+            "rows": 256, "vocab": 102400, "kernel": kernel, "kernel_b1": "small",
         },
         "hbm_gbps": h["wall_gbps"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
