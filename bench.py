@@ -159,15 +159,24 @@ def bench_latency(steps):
     e1.record(stream)
     hip.stream_sync(stream)
     b2b_us = e0.elapsed_ms(e1) * 1e3 / n_ev
-    # steady decode groups through the C generate loop
+    # steady decode groups through the C generate loop: result slots copied
+    # back per group (the reference's structure), then tokens through pinned
+    # host memory; both from the same state, so the tokens must agree
+    s.set_params(w.params, np.zeros(1, np.uint32))
+    s.set_history(w.history)
     toks_gen, r = G.generate(s, table, steps, rows=1, rng_mode=S.RNG_PHILOX)
+    s.set_params(w.params, np.zeros(1, np.uint32))
+    s.set_history(w.history)
+    toks_pin, rp = G.generate(s, table, steps, rows=1, rng_mode=S.RNG_PHILOX, pinned=pinned)
     s.close()
     pinned.free()
     for d in dev:
         d.free()
     return dict(steps=steps, launch_to_token_us_p50=pct(lat, 50), launch_to_token_us_p90=pct(lat, 90),
                 gpu_us_p50=pct(gpu_us, 50), gpu_us_p90=pct(gpu_us, 90), back_to_back_us_per_step=b2b_us,
-                decode_group_us_per_token=r["wall_us"] / max(r["emitted"], 1))
+                decode_group_us_per_token=r["wall_us"] / max(r["emitted"], 1),
+                decode_group_pinned_us_per_token=rp["wall_us"] / max(rp["emitted"], 1),
+                decode_group_tokens_agree=bool(toks_gen == toks_pin))
 
 
 def cpu_baseline(w, seconds):

@@ -62,6 +62,22 @@ pss_status pgl_generate(pss_sampler* s, const pgl_config* cfg, pgl_logits_fn log
                         pgl_emit_fn emit, void* ectx, pgl_result* out);
 
 /*
+ * pgl_generate with the tokens delivered through device-visible pinned host
+ * memory instead of a copy of the result slots: pass p of a group also
+ * stores its rows' tokens at pinned_dev[p * rows + row] (host view
+ * pinned_host, at least rows * PGL_DECODE_GROUP u32), and after enqueueing a
+ * group the host spins until the last pass's row-0 token lands (passes are
+ * stream-ordered, so the earlier ones have landed too).  The result slots are
+ * still written on the device.  Same tokens and state as pgl_generate; the
+ * group turnaround has no copy and no stream synchronization.  A token that
+ * has not landed after 2 s ends the loop with the stream's status (or
+ * PSS_ERR_HIP).
+ */
+pss_status pgl_generate_pinned(pss_sampler* s, const pgl_config* cfg, pgl_logits_fn logits, void* lctx,
+                               pgl_emit_fn emit, void* ectx, uint32_t* pinned_dev,
+                               volatile uint32_t* pinned_host, pgl_result* out);
+
+/*
  * Launch-to-token latency: `steps` single-row passes; each enqueues with the
  * token also stored into device-visible pinned host memory (`pinned_dev`, whose
  * host view is `pinned_host`) and spins on the host until it lands.

@@ -83,6 +83,94 @@ pss_status pgl_generate(pss_sampler* s, const pgl_config* cfg, pgl_logits_fn log
     return PSS_OK;
 }
 
+/* Spin until pinned[0] differs from the sentinel; 0 when it landed, else the
+ * stream's status after 2 s (a failed stream reports it; otherwise
+ * PSS_ERR_HIP). */
+static pss_status wait_token(pss_sampler* s, uint32_t rows, volatile uint32_t* pinned) {
+    double t0 = 0.0;
+    for (uint32_t n = 1;; ++n) {
+        if (__atomic_load_n(pinned, __ATOMIC_ACQUIRE) != 0xFFFFFFFFu) return PSS_OK;
+        if ((n & 4095u) == 0u) {
+            const double t = now_us();
+            if (t0 == 0.0) t0 = t;
+            else if (t - t0 > 2e6) {
+                const pss_status st = pss_read_results(s, rows, NULL, NULL);
+                if (__atomic_load_n(pinned, __ATOMIC_ACQUIRE) != 0xFFFFFFFFu) return PSS_OK;
+                return st != PSS_OK ? st : PSS_ERR_HIP;
+            }
+        }
+    }
+}
+
+pss_status pgl_generate_pinned(pss_sampler* s, const pgl_config* cfg, pgl_logits_fn logits, void* lctx,
+                               pgl_emit_fn emit, void* ectx, uint32_t* pinned_dev,
+                               volatile uint32_t* pinned_host, pgl_result* out) {
+    if (!s || !cfg || !logits || !emit || !out || !pinned_dev || !pinned_host || cfg->max_new == 0 ||
+        cfg->rows == 0 || cfg->rows > 256)
+        return PSS_ERR_INVALID_ARG;
+    const uint32_t rows = cfg->rows;
+    pgl_result r = {0, 1, 0, 0.0};
+    double t0 = now_us();
+    uint32_t pos = cfg->start_pos;
+    pss_status st;
+    pss_enqueue_opts o = {NULL, NULL, NULL, 0, NULL, 0, NULL};
+
+    /* prefill-final pass: slot 0, no position increment (generate.c:642) */
+    uint32_t posv[256];
+    for (uint32_t i = 0; i < rows; ++i) posv[i] = pos;
+    st = pss_set_position(s, 0, rows, posv);
+    if (st != PSS_OK) return st;
+    pinned_host[0] = 0xFFFFFFFFu;
+    __atomic_thread_fence(__ATOMIC_SEQ_CST);
+    o.host_tokens = pinned_dev;
+    st = pss_enqueue_ex(s, logits(lctx, pos), cfg->dtype, cfg->row_stride, rows, cfg->mode, 0, 0,
+                        cfg->rng_mode, &o);
+    if (st != PSS_OK) return st;
+    st = wait_token(s, rows, &pinned_host[0]);
+    if (st != PSS_OK) return st;
+    uint32_t tok = pinned_host[0];
+    r.emitted = 1;
+    int stop = emit(ectx, tok);
+    if (tok == cfg->eos || stop) {
+        r.finish_reason = 0;
+        r.wall_us = now_us() - t0;
+        *out = r;
+        return pss_read_results(s, rows, NULL, NULL);
+    }
+
+    uint32_t remaining = cfg->max_new - 1;
+    while (remaining > 0) {
+        uint32_t cur = remaining < PGL_DECODE_GROUP ? remaining : PGL_DECODE_GROUP;
+        for (uint32_t p = 0; p < cur; ++p) pinned_host[p * rows] = 0xFFFFFFFFu;
+        __atomic_thread_fence(__ATOMIC_SEQ_CST);
+        for (uint32_t p = 0; p < cur; ++p) {
+            o.host_tokens = pinned_dev + p * rows;
+            st = pss_enqueue_ex(s, logits(lctx, pos + p), cfg->dtype, cfg->row_stride, rows, cfg->mode, 1,
+                                p, cfg->rng_mode, &o);
+            if (st != PSS_OK) return st;
+        }
+        r.groups++;
+        st = wait_token(s, rows, &pinned_host[(cur - 1) * rows]);
+        if (st != PSS_OK) return st;
+        pos += cur;
+        for (uint32_t j = 0; j < cur; ++j) {
+            tok = pinned_host[j * rows]; /* row 0, pass j */
+            r.emitted++;
+            remaining--;
+            stop = emit(ectx, tok);
+            if (tok == cfg->eos || stop) {
+                r.finish_reason = 0;
+                remaining = 0;
+                break;
+            }
+        }
+    }
+    r.wall_us = now_us() - t0;
+    *out = r;
+    /* the state writes of the last passes are stream-ordered: wait for them */
+    return pss_read_results(s, rows, NULL, NULL);
+}
+
 pss_status pgl_step_latency(pss_sampler* s, pgl_logits_fn logits, void* lctx, uint32_t dtype,
                             uint64_t row_stride, uint32_t rng_mode, uint32_t steps,
                             uint32_t* pinned_dev, volatile uint32_t* pinned_host, double* lat_us,

@@ -431,6 +431,98 @@ __device__ __forceinline__ void pss_wave_tail4(const pss_args& a, uint32_t row, 
 }
 
 /*
+ * Finisher tail for 1..64 entries (src) that hold every element at or above
+ * the K-th largest, run by wave 0, one entry per lane: a 32-bit DPP/permlane
+ * sort of the keys in descending order gives the K-th largest (position
+ * K - 1, when `find_k`; otherwise tauK is exact already) and the key-order
+ * mass scan for the top-p cut (every quantity depends on the key alone, so
+ * ties need no order); min-p and the masses on each lane's own entry; a
+ * 32-bit sort of (id << 6) | lane orders the kept ids, their masses come from
+ * the owning lanes (ds_bpermute), and the first id whose cumulative mass
+ * exceeds the draw target is the token.
+ */
+__device__ __forceinline__ void pss_wave_tail64(const pss_args& a, uint32_t row, const pss_rowcfg& c,
+                                                const unsigned long long* src, uint32_t cnt, uint32_t tauK,
+                                                bool find_k, const pss_row_pre& pre, uint32_t u24,
+                                                uint32_t newRng) {
+    const uint32_t lane = pss_tid() & 63u;
+    const bool valid = lane < cnt;
+    const uint64_t my = valid ? src[lane] : 0ull;
+    const uint32_t mkey = (uint32_t)(my >> 32), mid = (uint32_t)my;
+    /* S5/S6 over the keys in descending order (keys of entries are at
+     * least key(-inf) > 0; missing lanes sort last as key 0).  Every
+     * quantity here depends on the key alone, so ties need no order. */
+    const uint32_t skey = ~dpp_sort_asc_u32(valid ? ~mkey : 0xFFFFFFFFu);
+    const uint32_t tmaxKey = wave_read_u32(skey, 0u);
+    if (find_k) tauK = wave_read_u32(skey, (c.K <= cnt ? c.K : cnt) - 1u);
+    const bool sv = valid && skey >= tauK;
+    const float tmax = pss_unkey(tmaxKey);
+    const uint64_t sq = sv ? pss_fixq(pss_prob(pss_unkey(skey), tmax)) : 0ull;
+    const uint64_t P = wave_incl_scan_u64(sq);
+    const uint64_t zk = wave_read_u64(P, 63);
+    uint32_t tau = tauK;
+    if (c.useTopP) {
+        const uint64_t need = pss_topp_need(c.topP, zk);
+        const uint64_t m = __ballot(sv && P >= need);
+        const uint32_t tauP = wave_read_u32(skey, (uint32_t)__ffsll((long long)m) - 1u);
+        tau = tauP > tau ? tauP : tau;
+    }
+    /* S7 on each lane's own entry */
+    const float sp = valid ? pss_prob(pss_unkey(mkey), tmax) : 0.0f;
+    const bool kp = valid && mkey >= tau && (!c.useMinP || sp >= c.minP);
+    const uint64_t kq = kp ? pss_fixq(sp) : 0ull;
+    const uint64_t Z = wave_sum_u64(kq);
+    const uint32_t keptCount = (uint32_t)__popcll(__ballot(kp));
+    const uint32_t lastAll = wave_max_u32(kp ? mid + 1u : 0u);
+    const uint32_t sid = mid;
+
+    /* S8: kept entries in id order ((id << 6) | lane: ids < 2^18), their
+     * masses fetched from the owning lanes, cumulative mass, first
+     * crossing */
+    const uint64_t target = pss_draw_target(u24, Z);
+    const uint32_t ix = dpp_sort_asc_u32(kp ? ((mid << 6) | lane) : 0xFFFFFFFFu);
+    const bool iv = ix != 0xFFFFFFFFu;
+    const int from = (int)((ix & 63u) << 2);
+    const uint32_t qlo = (uint32_t)__builtin_amdgcn_ds_bpermute(from, (int)(uint32_t)kq);
+    const uint32_t qhi = (uint32_t)__builtin_amdgcn_ds_bpermute(from, (int)(uint32_t)(kq >> 32));
+    const uint64_t C = wave_incl_scan_u64(iv ? (((uint64_t)qhi << 32) | qlo) : 0ull);
+    const uint64_t hit = __ballot(iv && C > target);
+    uint32_t tok, flags = 0;
+    if (hit) {
+        tok = wave_read_u32(ix, (uint32_t)__ffsll((long long)hit) - 1u) >> 6;
+    } else {
+        tok = lastAll > 0u ? lastAll - 1u : 0u;
+        flags |= PSS_INFO_FALLBACK;
+    }
+
+    /* verification outputs */
+    if (a.kept_mask || a.probs) {
+        if (a.kept_mask)
+            for (uint32_t w = lane; w < a.mask_words; w += 64u) a.kept_mask[(size_t)row * a.mask_words + w] = 0u;
+        if (a.probs)
+            for (uint32_t j = lane; j < a.V; j += 64u) a.probs[(size_t)row * a.probs_stride + j] = 0.0f;
+        pss_wait_mem();
+        if (kp) {
+            if (a.kept_mask) atomicOr(&a.kept_mask[(size_t)row * a.mask_words + (sid >> 5)], 1u << (sid & 31u));
+            if (a.probs) a.probs[(size_t)row * a.probs_stride + sid] = sp / ((float)Z * 0x1.0p-45f);
+        }
+    }
+    if (lane == 0) {
+        pss_row_info inf = {};
+        inf.token = tok;
+        inf.kept_count = keptCount;
+        inf.tau_key = tau;
+        inf.tmax_key = tmaxKey;
+        inf.z_kept = Z;
+        inf.z_topk = zk;
+        inf.target = target;
+        inf.u24 = u24;
+        inf.flags = flags;
+        pss_epilogue_pre(a, row, tok, false, c.W, newRng, inf, pre.pos, pre.step);
+    }
+}
+
+/*
  * Fast finisher for up to PSS_FAST_N candidates (list), those
  * below the row-wide bound G ignored (G is at most the K-th largest value,
  * so every entry of the top-K is at or above it):
@@ -600,83 +692,7 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
         }
     }
     if (cnt == 0u) return false;
-
-    if (tid < 64) {
-        const bool valid = lane < cnt;
-        const uint64_t my = valid ? src[lane] : 0ull;
-        const uint32_t mkey = (uint32_t)(my >> 32), mid = (uint32_t)my;
-        /* S5/S6 over the keys in descending order (keys of entries are at
-         * least key(-inf) > 0; missing lanes sort last as key 0).  Every
-         * quantity here depends on the key alone, so ties need no order. */
-        const uint32_t skey = ~dpp_sort_asc_u32(valid ? ~mkey : 0xFFFFFFFFu);
-        const uint32_t tmaxKey = wave_read_u32(skey, 0u);
-        if (nc <= 64u || coarse) tauK = wave_read_u32(skey, (c.K <= cnt ? c.K : cnt) - 1u);
-        const bool sv = valid && skey >= tauK;
-        const float tmax = pss_unkey(tmaxKey);
-        const uint64_t sq = sv ? pss_fixq(pss_prob(pss_unkey(skey), tmax)) : 0ull;
-        const uint64_t P = wave_incl_scan_u64(sq);
-        const uint64_t zk = wave_read_u64(P, 63);
-        uint32_t tau = tauK;
-        if (c.useTopP) {
-            const uint64_t need = pss_topp_need(c.topP, zk);
-            const uint64_t m = __ballot(sv && P >= need);
-            const uint32_t tauP = wave_read_u32(skey, (uint32_t)__ffsll((long long)m) - 1u);
-            tau = tauP > tau ? tauP : tau;
-        }
-        /* S7 on each lane's own entry */
-        const float sp = valid ? pss_prob(pss_unkey(mkey), tmax) : 0.0f;
-        const bool kp = valid && mkey >= tau && (!c.useMinP || sp >= c.minP);
-        const uint64_t kq = kp ? pss_fixq(sp) : 0ull;
-        const uint64_t Z = wave_sum_u64(kq);
-        const uint32_t keptCount = (uint32_t)__popcll(__ballot(kp));
-        const uint32_t lastAll = wave_max_u32(kp ? mid + 1u : 0u);
-        const uint32_t sid = mid;
-
-        /* S8: kept entries in id order ((id << 6) | lane: ids < 2^18), their
-         * masses fetched from the owning lanes, cumulative mass, first
-         * crossing */
-        const uint64_t target = pss_draw_target(u24, Z);
-        const uint32_t ix = dpp_sort_asc_u32(kp ? ((mid << 6) | lane) : 0xFFFFFFFFu);
-        const bool iv = ix != 0xFFFFFFFFu;
-        const int from = (int)((ix & 63u) << 2);
-        const uint32_t qlo = (uint32_t)__builtin_amdgcn_ds_bpermute(from, (int)(uint32_t)kq);
-        const uint32_t qhi = (uint32_t)__builtin_amdgcn_ds_bpermute(from, (int)(uint32_t)(kq >> 32));
-        const uint64_t C = wave_incl_scan_u64(iv ? (((uint64_t)qhi << 32) | qlo) : 0ull);
-        const uint64_t hit = __ballot(iv && C > target);
-        uint32_t tok, flags = 0;
-        if (hit) {
-            tok = wave_read_u32(ix, (uint32_t)__ffsll((long long)hit) - 1u) >> 6;
-        } else {
-            tok = lastAll > 0u ? lastAll - 1u : 0u;
-            flags |= PSS_INFO_FALLBACK;
-        }
-
-        /* verification outputs */
-        if (a.kept_mask || a.probs) {
-            if (a.kept_mask)
-                for (uint32_t w = lane; w < a.mask_words; w += 64u) a.kept_mask[(size_t)row * a.mask_words + w] = 0u;
-            if (a.probs)
-                for (uint32_t j = lane; j < a.V; j += 64u) a.probs[(size_t)row * a.probs_stride + j] = 0.0f;
-            pss_wait_mem();
-            if (kp) {
-                if (a.kept_mask) atomicOr(&a.kept_mask[(size_t)row * a.mask_words + (sid >> 5)], 1u << (sid & 31u));
-                if (a.probs) a.probs[(size_t)row * a.probs_stride + sid] = sp / ((float)Z * 0x1.0p-45f);
-            }
-        }
-        if (lane == 0) {
-            pss_row_info inf = {};
-            inf.token = tok;
-            inf.kept_count = keptCount;
-            inf.tau_key = tau;
-            inf.tmax_key = tmaxKey;
-            inf.z_kept = Z;
-            inf.z_topk = zk;
-            inf.target = target;
-            inf.u24 = u24;
-            inf.flags = flags;
-            pss_epilogue_pre(a, row, tok, false, c.W, newRng, inf, pre.pos, pre.step);
-        }
-    }
+    if (tid < 64) pss_wave_tail64(a, row, c, src, cnt, tauK, nc <= 64u || coarse, pre, u24, newRng);
     return true;
 }
 

@@ -36,6 +36,8 @@ def _lib():
         P, u32, u64 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64
         L.pgl_generate.argtypes = [P, P, P, P, P, P, P]
         L.pgl_generate.restype = ctypes.c_int
+        L.pgl_generate_pinned.argtypes = [P, P, P, P, P, P, P, P, P]
+        L.pgl_generate_pinned.restype = ctypes.c_int
         L.pgl_step_latency.argtypes = [P, P, P, u32, u64, u32, u32, P, P, P, P]
         L.pgl_step_latency.restype = ctypes.c_int
         L.pgl_table_logits.argtypes = [P, u32]
@@ -58,8 +60,10 @@ class LogitsTable:
 
 
 def generate(sampler, table, max_new, rows=1, dtype=S.DTYPE_F32, row_stride=None, mode=S.MODE_SAMPLE,
-             rng_mode=S.RNG_XORSHIFT32, eos=0xFFFFFFFF, start_pos=0, stop_after=None):
-    """pgl_generate; returns (emitted tokens of row 0, result dict)."""
+             rng_mode=S.RNG_XORSHIFT32, eos=0xFFFFFFFF, start_pos=0, stop_after=None, pinned=None):
+    """pgl_generate (or, with `pinned` a hip.PinnedBuffer of at least
+    rows * 4 u32, pgl_generate_pinned); returns (emitted tokens of row 0,
+    result dict)."""
     out = []
 
     def _emit(ctx, tok):
@@ -69,10 +73,17 @@ def generate(sampler, table, max_new, rows=1, dtype=S.DTYPE_F32, row_stride=None
     emit = EMIT_FN(_emit)
     cfg = CConfig(max_new, eos, rows, dtype, row_stride or sampler.vocab, mode, rng_mode, start_pos)
     res = CResult()
-    st = _lib().pgl_generate(sampler.handle, ctypes.byref(cfg), table.fn, table.ctx,
-                             ctypes.cast(emit, ctypes.c_void_p), None, ctypes.byref(res))
+    if pinned is None:
+        st = _lib().pgl_generate(sampler.handle, ctypes.byref(cfg), table.fn, table.ctx,
+                                 ctypes.cast(emit, ctypes.c_void_p), None, ctypes.byref(res))
+    else:
+        if pinned.nbytes < 4 * rows * 4:
+            raise ValueError("pinned buffer smaller than rows * 4 u32")
+        st = _lib().pgl_generate_pinned(sampler.handle, ctypes.byref(cfg), table.fn, table.ctx,
+                                        ctypes.cast(emit, ctypes.c_void_p), None, pinned.dev_ptr, pinned.ptr,
+                                        ctypes.byref(res))
     if st != 0:
-        raise S.PssError(st, "pgl_generate")
+        raise S.PssError(st, "pgl_generate" if pinned is None else "pgl_generate_pinned")
     return out, dict(emitted=res.emitted, finish_reason=res.finish_reason, groups=res.groups,
                      wall_us=res.wall_us)
 
