@@ -78,6 +78,19 @@ pss_status pgl_generate_pinned(pss_sampler* s, const pgl_config* cfg, pgl_logits
                                volatile uint32_t* pinned_host, pgl_result* out);
 
 /*
+ * Scoring consumption of generateScore (src/generate.c:1198-1228) for row 0:
+ * ids[0..n) are scored in groups of PGL_DECODE_GROUP passes; per group the
+ * targets go to the pass slots (pss_set_score_targets, the reference's
+ * tokenIds[1 + p] writes), pass p reads the logits at position
+ * start_pos + j (j = the id's index) with PSS_MODE_SCORE and do_increment 1,
+ * and the group's result slots are read back as float losses and summed in
+ * binary64 in id order.  *loss_sum and *count as generateScore's outLoss and
+ * outCount.
+ */
+pss_status pgl_score(pss_sampler* s, pgl_logits_fn logits, void* lctx, uint32_t dtype, uint64_t row_stride,
+                     const uint32_t* ids, uint32_t n, uint32_t start_pos, double* loss_sum, uint64_t* count);
+
+/*
  * Launch-to-token latency: `steps` single-row passes; each enqueues with the
  * token also stored into device-visible pinned host memory (`pinned_dev`, whose
  * host view is `pinned_host`) and spins on the host until it lands.

@@ -61,7 +61,10 @@ typedef enum { PSS_DTYPE_F32 = 0, PSS_DTYPE_F16 = 1 } pss_dtype;
 
 /* ArgMax-Reduce.comp push constant `mode` (0 greedy, 1 sample).  SAMPLE picks
  * greedy per row when that row's temperature is not > 0 (generate.c:1418). */
-typedef enum { PSS_MODE_GREEDY = 0, PSS_MODE_SAMPLE = 1 } pss_mode;
+/* PSS_MODE_SCORE: ArgMax-Reduce.comp mode 2 (:169-214), the negative
+ * log-likelihood of a given target (pss_set_score_targets) as float bits in
+ * the result slot; generateScore, src/generate.c:1161-1236. */
+typedef enum { PSS_MODE_GREEDY = 0, PSS_MODE_SAMPLE = 1, PSS_MODE_SCORE = 2 } pss_mode;
 
 /* Uniform source of the draw.
  *   XORSHIFT32: the reference stream: s = rng (0 -> 0x9E3779B9), u = (s>>8)/2^24,
@@ -85,6 +88,7 @@ typedef struct {
 
 #define PSS_INFO_GREEDY 1u     /* row was decoded greedily                    */
 #define PSS_INFO_FALLBACK 2u   /* no id crossed the target; last kept id used */
+#define PSS_INFO_SCORE 4u      /* scoring pass: z_kept = Zq of all ids, tmax_key = key(gmax) */
 
 typedef struct pss_sampler pss_sampler;
 
@@ -148,13 +152,27 @@ pss_status pss_reset_history(pss_sampler* s, uint32_t row0, uint32_t rows, uint3
 pss_status pss_set_history(pss_sampler* s, uint32_t row0, uint32_t rows,
                            const uint32_t* hist, uint32_t len);
 
+/*
+ * Targets of scoring passes (PSS_MODE_SCORE): ids[r * slots + k] is the token
+ * scored by pass slot k (pass_idx = k, 0 <= k < slots <= PSS_RESULT_SLOTS) of
+ * row row0 + r.  Replaces the host writes of tokenIds[1 + p] before each
+ * group in generateScore (src/generate.c:1190, :1208) and the shader's read
+ * of tokenIds[1 + passIdx] (ArgMax-Reduce.comp:196).  Synchronous with the
+ * sampler's stream (the caller's array may be reused on return).  Ids >= V
+ * score against a logit of 0, as the shader does.
+ */
+pss_status pss_set_score_targets(pss_sampler* s, uint32_t row0, uint32_t rows, uint32_t slots,
+                                 const uint32_t* ids);
+
 pss_status pss_set_position(pss_sampler* s, uint32_t row0, uint32_t rows, const uint32_t* pos);
 
 /*
  * One sampler step over `rows` logit rows (state rows 0..rows-1).
  *   logits      device pointer, row r at logits + r*row_stride elements
  *   dtype       PSS_DTYPE_F32 or PSS_DTYPE_F16
- *   mode        PSS_MODE_SAMPLE (per-row greedy when T <= 0) or PSS_MODE_GREEDY
+ *   mode        PSS_MODE_SAMPLE (per-row greedy when T <= 0), PSS_MODE_GREEDY, or
+ *               PSS_MODE_SCORE (result slot = float bits of the target's NLL,
+ *               token = the target; history, rng and step untouched)
  *   do_increment  1: position += 1 after the step (ArgMax-Reduce.comp:384)
  *   pass_idx    result slot 0..3 written (ArgMax-Reduce.comp:377)
  *   rng_mode    pss_rng_mode

@@ -102,6 +102,10 @@ def lib():
         L.oracle_fixq.argtypes = [f32]
         L.oracle_h2f.restype = f32
         L.oracle_h2f.argtypes = [ctypes.c_uint16]
+        L.oracle_o1_score_row.restype = f32
+        L.oracle_o1_score_row.argtypes = [P, u32, u32, P, P]
+        L.oracle_log64.restype = ctypes.c_double
+        L.oracle_log64.argtypes = [ctypes.c_double]
         _lib = L
     return _lib
 
@@ -183,6 +187,20 @@ def o1_batch(logits, params, history, position, rng, step, mode=1, rng_mode=0, d
                           _ptr(rng), _ptr(step), mode, rng_mode, do_increment, _ptr(tokens),
                           _ptr(infos), int(threads))
     return tokens, infos
+
+
+def o1_score_row(logits, target):
+    """Scoring mode on one row (fp32 values; fp16 rows widen exactly first).
+    Returns (nll as float32 bits, Zq, key of the row maximum)."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    zq = np.zeros(1, np.uint64)
+    gk = np.zeros(1, np.uint32)
+    nll = lib().oracle_o1_score_row(_ptr(x), x.size, int(target), _ptr(zq), _ptr(gk))
+    return int(np.float32(nll).view(np.uint32)), int(zq[0]), int(gk[0])
+
+
+def log64(x):
+    return lib().oracle_log64(float(x))
 
 
 def o2_shader_row(logits, params, history, position, rng, do_increment=1):

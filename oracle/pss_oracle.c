@@ -689,6 +689,30 @@ uint32_t oracle_o3_sampler_ref(float* logits, int V, const sample_params* sp, ui
 /* src/data.c:8-28                                                          */
 /* ------------------------------------------------------------------------ */
 
+/*
+ * Scoring mode (ArgMax-Reduce.comp:169-214), build contract: raw logits made
+ * canonical (NaN -> -inf, -0 -> +0), gmax their maximum, Zq the exact
+ * fixed-point sum of exp(t - gmax), lt the target's value (0 when target >=
+ * V, as the shader's sumAll over no match), nll = log(Z) + gmax - lt
+ * (pss_score_nll).  Plain loops in id order.
+ */
+float oracle_o1_score_row(const float* logits, uint32_t V, uint32_t target, uint64_t* zq_out,
+                          uint32_t* gmax_key_out) {
+    float gmax = pss_u2f(0xFF800000u);
+    for (uint32_t j = 0; j < V; ++j) {
+        const float t = pss_canon(logits[j]);
+        if (pss_key(t) > pss_key(gmax)) gmax = t;
+    }
+    uint64_t zq = 0;
+    for (uint32_t j = 0; j < V; ++j) zq += pss_fixq(pss_prob(pss_canon(logits[j]), gmax));
+    const float lt = target < V ? pss_canon(logits[target]) : 0.0f;
+    if (zq_out) *zq_out = zq;
+    if (gmax_key_out) *gmax_key_out = pss_key(gmax);
+    return pss_score_nll(zq, gmax, lt);
+}
+
+double oracle_log64(double x) { return pss_log64(x); }
+
 float oracle_get_pseudo_random(int i, int j, int seed) {
     /* The original forms i*73129 + j*95121 + seed*15473 in int and converts to
      * unsigned; done here in uint32_t so the wrap is defined. */

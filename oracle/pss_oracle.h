@@ -72,6 +72,10 @@ uint64_t oracle_exp_scan(float lo, float hi, uint32_t acc_stride, double* max_ul
 
 float oracle_pss_exp(float x);
 void oracle_exp_many(const float* x, float* y, uint64_t n);
+/* Scoring mode on one fp32 row; returns the NLL, Zq and key(gmax) optional. */
+float oracle_o1_score_row(const float* logits, uint32_t V, uint32_t target, uint64_t* zq_out,
+                          uint32_t* gmax_key_out);
+double oracle_log64(double x);
 void oracle_prob_many(const float* t, float tmax, float* y, uint64_t n);
 void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
 uint32_t oracle_xorshift32(uint32_t x);

@@ -10,6 +10,7 @@
 #include "pumice_generate.h"
 
 #include <stddef.h>
+#include <string.h>
 #include <time.h>
 
 static double now_us(void) {
@@ -169,6 +170,38 @@ pss_status pgl_generate_pinned(pss_sampler* s, const pgl_config* cfg, pgl_logits
     *out = r;
     /* the state writes of the last passes are stream-ordered: wait for them */
     return pss_read_results(s, rows, NULL, NULL);
+}
+
+pss_status pgl_score(pss_sampler* s, pgl_logits_fn logits, void* lctx, uint32_t dtype, uint64_t row_stride,
+                     const uint32_t* ids, uint32_t n, uint32_t start_pos, double* loss_sum, uint64_t* count) {
+    if (!s || !logits || (!ids && n) || !loss_sum || !count) return PSS_ERR_INVALID_ARG;
+    double sum = 0.0;
+    uint64_t cnt = 0;
+    uint32_t posv[1] = {start_pos};
+    pss_status st = pss_set_position(s, 0, 1, posv);
+    if (st != PSS_OK) return st;
+    uint32_t results[PSS_RESULT_SLOTS];
+    for (uint32_t j = 0; j < n; j += PGL_DECODE_GROUP) {
+        const uint32_t cur = n - j < PGL_DECODE_GROUP ? n - j : PGL_DECODE_GROUP;
+        st = pss_set_score_targets(s, 0, 1, cur, ids + j);
+        if (st != PSS_OK) return st;
+        for (uint32_t p = 0; p < cur; ++p) {
+            st = pss_enqueue(s, logits(lctx, start_pos + j + p), dtype, row_stride, 1, PSS_MODE_SCORE, 1, p,
+                             PSS_RNG_XORSHIFT32);
+            if (st != PSS_OK) return st;
+        }
+        st = pss_read_results(s, 1, results, NULL);
+        if (st != PSS_OK) return st;
+        for (uint32_t p = 0; p < cur; ++p) {
+            float loss;
+            memcpy(&loss, &results[p], sizeof loss);
+            sum += (double)loss;
+            cnt++;
+        }
+    }
+    *loss_sum = sum;
+    *count = cnt;
+    return PSS_OK;
 }
 
 pss_status pgl_step_latency(pss_sampler* s, pgl_logits_fn logits, void* lctx, uint32_t dtype,

@@ -135,6 +135,62 @@ PSS_HD float pss_prob(float t, float tmax) {
 /* Fixed-point mass: p in [0, 1] -> trunc(p * 2^45).  p * 2^45 is exact. */
 PSS_HD uint64_t pss_fixq(float p) { return (uint64_t)(p * 0x1.0p45f); }
 
+/*
+ * Natural log of a finite binary64 x >= 2^-1022 (the scoring mode takes it of
+ * Z in [1, 2^18]), the same bits on the CPU and the GPU: plain IEEE adds,
+ * multiplies and one division, no fused operations.  The reduction of
+ * fdlibm's e_log.c (Sun Microsystems, 1993): x = (1 + f) * 2^k with 1 + f in
+ * [sqrt(1/2), sqrt(2)), s = f / (2 + f), log(1 + f) = f - (hfsq - s (hfsq +
+ * R)) with hfsq = f^2 / 2 and R = 2 atanh(s) / s - 2 = z (2/3 + 2/5 z + ...)
+ * (z = s^2 <= 0.0295), here the Taylor series through z^12 instead of
+ * fdlibm's minimax polynomial; ln2 split hi + lo (hi has 36 significant bits,
+ * so k * hi is exact for |k| < 2^17).  Under one unit in the last place.
+ */
+PSS_HD double pss_log64(double x) {
+    uint64_t b;
+    __builtin_memcpy(&b, &x, sizeof b);
+    int k = (int)((b >> 52) & 0x7FFu) - 1022; /* x = m * 2^k, m in [0.5, 1) */
+    b = (b & 0x000FFFFFFFFFFFFFull) | 0x3FE0000000000000ull;
+    double m;
+    __builtin_memcpy(&m, &b, sizeof m);
+    if (m < 0x1.6a09e667f3bcdp-1) { /* sqrt(1/2) */
+        m = m * 2.0;
+        k = k - 1;
+    }
+    const double f = m - 1.0;
+    const double s = f / (2.0 + f);
+    const double z = s * s;
+    double R = 2.0 / 25.0;
+    R = R * z + 2.0 / 23.0;
+    R = R * z + 2.0 / 21.0;
+    R = R * z + 2.0 / 19.0;
+    R = R * z + 2.0 / 17.0;
+    R = R * z + 2.0 / 15.0;
+    R = R * z + 2.0 / 13.0;
+    R = R * z + 2.0 / 11.0;
+    R = R * z + 2.0 / 9.0;
+    R = R * z + 2.0 / 7.0;
+    R = R * z + 2.0 / 5.0;
+    R = R * z + 2.0 / 3.0;
+    R = R * z;
+    const double hfsq = 0.5 * f * f;
+    const double ln2_hi = 0x1.62e42fefap-1;      /* 36 significant bits */
+    const double ln2_lo = 0x1.cf79abc9e3b3ap-40; /* ln2 - ln2_hi */
+    const double dk = (double)k;
+    return dk * ln2_hi - ((hfsq - (s * (hfsq + R) + dk * ln2_lo)) - f);
+}
+
+/*
+ * Scoring (ArgMax-Reduce.comp mode 2, :169-214): the negative log-likelihood
+ * of `lt` under the row's raw logits, log(Z) + gmax - lt, from the exact
+ * fixed-point mass Zq = sum fixq(exp(t - gmax)) (Z = Zq * 2^-45), evaluated in
+ * binary64 and rounded once to binary32.
+ */
+PSS_HD float pss_score_nll(uint64_t Zq, float gmax, float lt) {
+    const double Z = (double)Zq * 0x1.0p-45;
+    return (float)((pss_log64(Z) + (double)gmax) - (double)lt);
+}
+
 PSS_HD uint32_t pss_xorshift32(uint32_t x) {
     x ^= x << 13;
     x ^= x >> 17;

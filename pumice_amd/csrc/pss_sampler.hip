@@ -13,6 +13,7 @@
 #include <string.h>
 
 #include "pss_general.h"
+#include "pss_score.h"
 #include "pss_stream.h"
 #include "pumice_sampler.h"
 
@@ -29,6 +30,7 @@ struct pss_sampler {
     uint32_t* d_hist;
     uint32_t* d_result;
     uint32_t* d_tokens;
+    uint32_t* d_targets; /* scoring targets [max_rows][PSS_RESULT_SLOTS] */
     void* d_ws;       /* streaming-kernel workspace: per-row bounds and candidate pools */
     size_t ws_bytes;
     uint32_t* h_topk; /* host copy of each row's topK (picks the kernel variant) */
@@ -76,6 +78,7 @@ static void free_all(pss_sampler* s) {
     (void)hipFree(s->d_hist);
     (void)hipFree(s->d_result);
     (void)hipFree(s->d_tokens);
+    (void)hipFree(s->d_targets);
     (void)hipFree(s->d_ws);
     free(s->h_topk);
     if (s->own_stream && s->stream) (void)hipStreamDestroy(s->stream);
@@ -123,6 +126,7 @@ extern "C" pss_status pss_create(pss_sampler** out, uint32_t vocab, uint32_t max
         hipMalloc((void**)&s->d_hist, 4 * R * PSS_MAX_PENALTY_LEN) != hipSuccess ||
         hipMalloc((void**)&s->d_result, 4 * R * PSS_RESULT_SLOTS) != hipSuccess ||
         hipMalloc((void**)&s->d_tokens, 4 * R) != hipSuccess ||
+        hipMalloc((void**)&s->d_targets, 4 * R * PSS_RESULT_SLOTS) != hipSuccess ||
         (s->ws_bytes && hipMalloc(&s->d_ws, s->ws_bytes) != hipSuccess)) {
         free_all(s);
         return PSS_ERR_ALLOC;
@@ -135,6 +139,7 @@ extern "C" pss_status pss_create(pss_sampler** out, uint32_t vocab, uint32_t max
     if (st == PSS_OK) st = fill_u32(s->stream, s->d_hist, R * PSS_MAX_PENALTY_LEN, PSS_SENTINEL);
     if (st == PSS_OK) st = fill_u32(s->stream, s->d_result, R * PSS_RESULT_SLOTS, 0u);
     if (st == PSS_OK) st = fill_u32(s->stream, s->d_tokens, R, 0u);
+    if (st == PSS_OK) st = fill_u32(s->stream, s->d_targets, R * PSS_RESULT_SLOTS, 0u);
     if (st == PSS_OK && s->ws_bytes) st = fill_u32(s->stream, (uint32_t*)s->d_ws, s->ws_bytes / 4, 0u);
     if (st == PSS_OK && hipStreamSynchronize(s->stream) != hipSuccess) st = PSS_ERR_HIP;
     if (st != PSS_OK) {
@@ -208,6 +213,15 @@ extern "C" pss_status pss_set_history(pss_sampler* s, uint32_t row0, uint32_t ro
     return st;
 }
 
+extern "C" pss_status pss_set_score_targets(pss_sampler* s, uint32_t row0, uint32_t rows, uint32_t slots,
+                                            const uint32_t* ids) {
+    if (!rows_ok(s, row0, rows) || !ids || slots == 0 || slots > PSS_RESULT_SLOTS) return PSS_ERR_INVALID_ARG;
+    HIP_TRY(hipMemcpy2DAsync(s->d_targets + (size_t)row0 * PSS_RESULT_SLOTS, 4u * PSS_RESULT_SLOTS, ids,
+                             4u * slots, 4u * slots, rows, hipMemcpyHostToDevice, s->stream));
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    return PSS_OK;
+}
+
 extern "C" pss_status pss_set_position(pss_sampler* s, uint32_t row0, uint32_t rows,
                                        const uint32_t* pos) {
     if (!rows_ok(s, row0, rows) || !pos) return PSS_ERR_INVALID_ARG;
@@ -259,11 +273,21 @@ extern "C" pss_status pss_enqueue_ex(pss_sampler* s, const void* logits, uint32_
                                      const pss_enqueue_opts* opts) {
     if (!s || !logits || rows == 0 || rows > s->max_rows) return PSS_ERR_INVALID_ARG;
     if (dtype != PSS_DTYPE_F32 && dtype != PSS_DTYPE_F16) return PSS_ERR_INVALID_ARG;
-    if (mode != PSS_MODE_GREEDY && mode != PSS_MODE_SAMPLE) return PSS_ERR_INVALID_ARG;
+    if (mode != PSS_MODE_GREEDY && mode != PSS_MODE_SAMPLE && mode != PSS_MODE_SCORE) return PSS_ERR_INVALID_ARG;
     if (rng_mode != PSS_RNG_XORSHIFT32 && rng_mode != PSS_RNG_PHILOX) return PSS_ERR_INVALID_ARG;
     if (pass_idx >= PSS_RESULT_SLOTS || row_stride < s->V) return PSS_ERR_INVALID_ARG;
     if (opts && opts->probs && opts->probs_stride < s->V) return PSS_ERR_INVALID_ARG;
     pss_args a = make_args(s, logits, dtype, row_stride, mode, do_increment, pass_idx, rng_mode, opts);
+    if (mode == PSS_MODE_SCORE) {
+        const size_t esz = dtype == PSS_DTYPE_F16 ? 2u : 4u;
+        a.vec_ok = ((a.stride * esz) % 16u == 0u) && (((uintptr_t)a.logits & 15u) == 0u) &&
+                   ((a.V * esz) % 16u == 0u);
+        if (dtype == PSS_DTYPE_F16)
+            pss_score_kernel<PSS_DTYPE_F16><<<dim3(rows), dim3(PSS_SCORE_NT), 0, s->stream>>>(a, s->d_targets);
+        else
+            pss_score_kernel<PSS_DTYPE_F32><<<dim3(rows), dim3(PSS_SCORE_NT), 0, s->stream>>>(a, s->d_targets);
+        return hipGetLastError() == hipSuccess ? PSS_OK : PSS_ERR_HIP;
+    }
     /* The streaming kernel, or the one-workgroup-per-row general kernel when
      * the caller asks for it (both compute identical results). */
     const int general = opts && (opts->flags & PSS_ENQ_GENERAL);

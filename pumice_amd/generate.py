@@ -38,6 +38,8 @@ def _lib():
         L.pgl_generate.restype = ctypes.c_int
         L.pgl_generate_pinned.argtypes = [P, P, P, P, P, P, P, P, P]
         L.pgl_generate_pinned.restype = ctypes.c_int
+        L.pgl_score.argtypes = [P, P, P, u32, u64, P, u32, u32, P, P]
+        L.pgl_score.restype = ctypes.c_int
         L.pgl_step_latency.argtypes = [P, P, P, u32, u64, u32, u32, P, P, P, P]
         L.pgl_step_latency.restype = ctypes.c_int
         L.pgl_table_logits.argtypes = [P, u32]
@@ -97,3 +99,15 @@ def step_latency(sampler, table, steps, pinned, dtype=S.DTYPE_F32, rng_mode=S.RN
     if st != 0:
         raise S.PssError(st, "pgl_step_latency")
     return lat, toks
+
+
+def score(sampler, table, ids, dtype=S.DTYPE_F32, row_stride=None, start_pos=0):
+    """pgl_score over ids (row 0); returns (loss_sum, count)."""
+    a = np.ascontiguousarray(ids, dtype=np.uint32)
+    loss = ctypes.c_double()
+    cnt = ctypes.c_uint64()
+    st = _lib().pgl_score(sampler.handle, table.fn, table.ctx, dtype, row_stride or sampler.vocab,
+                          a.ctypes.data, a.size, start_pos, ctypes.byref(loss), ctypes.byref(cnt))
+    if st != 0:
+        raise S.PssError(st, "pgl_score")
+    return loss.value, cnt.value

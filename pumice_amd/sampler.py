@@ -24,9 +24,9 @@ MAX_VOCAB = 262144
 SENTINEL = 0xFFFFFFFF
 
 DTYPE_F32, DTYPE_F16 = 0, 1
-MODE_GREEDY, MODE_SAMPLE = 0, 1
+MODE_GREEDY, MODE_SAMPLE, MODE_SCORE = 0, 1, 2
 RNG_XORSHIFT32, RNG_PHILOX = 0, 1
-INFO_GREEDY, INFO_FALLBACK = 1, 2
+INFO_GREEDY, INFO_FALLBACK, INFO_SCORE = 1, 2, 4
 ENQ_GENERAL = 1
 ENQ_SPLIT = 2
 ENQ_FUSED = 4
@@ -68,7 +68,7 @@ EXPORTS = [
     "pss_create", "pss_destroy", "pss_set_params", "pss_reset_history", "pss_set_history",
     "pss_set_position", "pss_enqueue", "pss_enqueue_ex", "pss_read_results", "pss_read_state",
     "pss_get_state_ptrs", "pss_sanitize_request", "pss_stream", "pss_status_string",
-    "pss_mask_words",
+    "pss_mask_words", "pss_set_score_targets",
 ]
 
 
@@ -94,6 +94,7 @@ def lib():
         L.pss_reset_history.argtypes = [P, u32, u32, u32]
         L.pss_set_history.argtypes = [P, u32, u32, P, u32]
         L.pss_set_position.argtypes = [P, u32, u32, P]
+        L.pss_set_score_targets.argtypes = [P, u32, u32, u32, P]
         L.pss_enqueue.argtypes = [P, P, u32, u64, u32, u32, u32, u32, u32]
         L.pss_enqueue_ex.argtypes = [P, P, u32, u64, u32, u32, u32, u32, u32, P]
         L.pss_read_results.argtypes = [P, u32, P, P]
@@ -192,6 +193,14 @@ class Sampler:
             h = h[None, :]
         _ok(lib().pss_set_history(self.handle, row0, h.shape[0], h.ctypes.data, h.shape[1]),
             "pss_set_history")
+
+    def set_score_targets(self, ids, row0=0):
+        """ids [rows][slots] (slots <= 4): the token scored by pass slot k of each row."""
+        t = np.ascontiguousarray(ids, dtype=np.uint32)
+        if t.ndim == 1:
+            t = t[:, None]
+        _ok(lib().pss_set_score_targets(self.handle, row0, t.shape[0], t.shape[1], t.ctypes.data),
+            "pss_set_score_targets")
 
     def set_position(self, pos, row0=0):
         p = np.ascontiguousarray(pos, dtype=np.uint32).reshape(-1)

@@ -15,6 +15,9 @@ Each check is chosen so a plausible mistake in the oracle fails it:
     reference's own acceptance rule (exact, or u*Z within 5e-4*Z of the
     token's CDF interval; src/validation.c:5075-5081).
   - Greedy one-stage against the reference's two-stage argmax structure.
+  - Scoring (mode 2): the binary64 log against libm (ulp bound, powers of two,
+    the range-reduction boundary), the NLL against an fp64 log-sum-exp, the
+    exact fixed-point mass against an fp64 sum, and the special rows.
 """
 import json
 import math
@@ -422,3 +425,74 @@ def test_configs_golden():
     assert [O.o1_row(xs[k, 0], w.params[0], st)["token"] for k in range(8)] == g["c2_chain"]
     st = O.RowState(w.history[0], 0, 99, 0)
     assert [O.o1_row(xs[k, 0], w.params[0], st, rng_mode=1)["token"] for k in range(8)] == g["c2_chain_philox"]
+
+
+def test_log64_against_libm():
+    """pss_log64 (shared by the scoring kernel and the oracle): within 1 ulp of
+    libm's log over 2^-20 .. 2^40, exact at powers of two, continuous across the
+    sqrt(1/2) range-reduction boundary.  A wrong series term or ln2 split
+    fails the ulp bound by orders of magnitude."""
+    rng = np.random.default_rng(5)
+    xs = np.concatenate([np.exp2(rng.uniform(-20, 40, 20000)), 1.0 + rng.uniform(-1e-3, 1e-3, 2000),
+                         [1.0, 2.0, 0.5, 3.0, 10.0, 262144.0, 2.0 ** 18 - 1, math.sqrt(0.5), math.sqrt(2.0)]])
+    worst = 0.0
+    for x in xs:
+        x = float(x)
+        got, ref = O.log64(x), math.log(x)
+        if ref == 0.0:
+            assert got == 0.0
+            continue
+        worst = max(worst, abs(got - ref) / math.ulp(ref))
+    assert worst <= 1.0, worst
+    for e in range(-30, 31):
+        assert O.log64(2.0 ** e) == e * math.log(2.0) or abs(O.log64(2.0 ** e) - e * math.log(2.0)) <= math.ulp(e * math.log(2.0))
+    b = math.sqrt(0.5)
+    lo, hi = np.nextafter(b, 0.0), np.nextafter(b, 1.0)
+    assert O.log64(float(lo)) < O.log64(b) <= O.log64(float(hi))
+
+
+def _nll64(x, target):
+    x = x.astype(np.float64)
+    m = x.max()
+    lt = x[target] if target < x.size else 0.0
+    return math.log(np.exp(x - m).sum()) + m - lt
+
+
+def test_score_oracle_against_fp64():
+    """O1 scoring = log(Z) + gmax - l[target] within fp32 rounding of an fp64
+    log-sum-exp; Zq * 2^-45 within binary32 rounding of the fp64 sum (each term
+    is a binary32 exp, then truncated to 2^-45); gmax its key."""
+    rng = np.random.default_rng(6)
+    for V in (1, 7, 1000, 4096, 102400):
+        for sigma in (0.5, 3.0, 20.0):
+            x = (rng.normal(0.0, sigma, V)).astype(np.float32)
+            for target in (0, V - 1, V // 2, V, V + 5):
+                bits, zq, gk = O.o1_score_row(x, target)
+                nll = float(np.uint32(bits).view(np.float32))
+                ref = _nll64(x, target)
+                assert abs(nll - ref) <= 2.0 * float(np.spacing(np.float32(abs(ref)))) + 1e-6 * abs(ref), (V, sigma, target)
+                z64 = np.exp(x.astype(np.float64) - float(x.max())).sum()
+                assert abs(zq * 2.0 ** -45 - z64) <= 2.0 ** -23 * z64 + V * 2.0 ** -45
+                assert gk == O.key(float(x.max()))
+
+
+def test_score_oracle_special_rows():
+    V = 64
+    x = np.zeros(V, np.float32)
+    bits, zq, _ = O.o1_score_row(x, 3)          # all equal: log V
+    assert np.uint32(bits).view(np.float32) == np.float32(math.log(V))
+    assert zq == V << 45
+    y = np.full(V, -np.inf, np.float32)
+    bits, _, _ = O.o1_score_row(y, 0)            # all -inf: -inf - (-inf)
+    assert np.isnan(np.uint32(bits).view(np.float32))
+    z = np.zeros(V, np.float32)
+    z[5] = np.inf
+    bits, zq, _ = O.o1_score_row(z, 6)           # +inf max, finite target
+    assert np.uint32(bits).view(np.float32) == np.float32(np.inf) and zq == 1 << 45
+    w = np.arange(V, dtype=np.float32)
+    w[9] = np.nan                                # NaN is -inf: contributes nothing
+    b1, _, _ = O.o1_score_row(w, 10)
+    w2 = w.copy()
+    w2[9] = -np.inf
+    b2, _, _ = O.o1_score_row(w2, 10)
+    assert b1 == b2
