@@ -52,6 +52,8 @@ struct pss_args {
     /* per-row workspace of the fast kernel (candidate pools, tickets) */
     void* ws;
     uint32_t vec_ok;      /* rows 16-byte aligned, V * element size a multiple of 16 */
+    uint32_t kmax_cov;    /* largest top-k the launched streaming form covers */
+    uint32_t wmax_cov;    /* largest window it covers */
 };
 
 /* Global-memory pointers.  Pointers that reach a kernel inside a struct are

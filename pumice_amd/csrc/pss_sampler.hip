@@ -34,6 +34,7 @@ struct pss_sampler {
     void* d_ws;       /* streaming-kernel workspace: per-row bounds and candidate pools */
     size_t ws_bytes;
     uint32_t* h_topk; /* host copy of each row's topK (picks the kernel variant) */
+    uint32_t* h_wlen; /* host copy of each row's penaltyLength (likewise) */
 };
 
 #define HIP_TRY(expr)                            \
@@ -81,6 +82,7 @@ static void free_all(pss_sampler* s) {
     (void)hipFree(s->d_targets);
     (void)hipFree(s->d_ws);
     free(s->h_topk);
+    free(s->h_wlen);
     if (s->own_stream && s->stream) (void)hipStreamDestroy(s->stream);
     free(s);
 }
@@ -114,7 +116,8 @@ extern "C" pss_status pss_create(pss_sampler** out, uint32_t vocab, uint32_t max
     }
     const size_t R = max_rows;
     s->h_topk = (uint32_t*)calloc(R, sizeof(uint32_t));
-    if (!s->h_topk) {
+    s->h_wlen = (uint32_t*)calloc(R, sizeof(uint32_t));
+    if (!s->h_topk || !s->h_wlen) {
         free_all(s);
         return PSS_ERR_ALLOC;
     }
@@ -182,7 +185,10 @@ extern "C" pss_status pss_set_params(pss_sampler* s, uint32_t row0, uint32_t row
     }
     pss_status st = upload_sync(s, s->d_params + row0, params, sizeof(sample_params) * rows);
     if (st != PSS_OK) return st;
-    for (uint32_t i = 0; i < rows; ++i) s->h_topk[row0 + i] = params[i].topK;
+    for (uint32_t i = 0; i < rows; ++i) {
+        s->h_topk[row0 + i] = params[i].topK;
+        s->h_wlen[row0 + i] = params[i].penaltyLength;
+    }
     if (seeds) {
         st = upload_sync(s, s->d_rng + row0, seeds, 4u * rows);
     } else {
@@ -257,6 +263,8 @@ static pss_args make_args(pss_sampler* s, const void* logits, uint32_t dtype, ui
     a.token_ids = s->d_tokens;
     a.mask_words = pss_mask_words(s->V);
     a.ws = s->d_ws;
+    a.kmax_cov = PSS_SEG_KMAX;
+    a.wmax_cov = PSS_SEG_WMAX;
     if (o) {
         a.info = o->row_info;
         a.kept_mask = o->kept_mask;
@@ -292,15 +300,18 @@ extern "C" pss_status pss_enqueue_ex(pss_sampler* s, const void* logits, uint32_
      * the caller asks for it (both compute identical results). */
     const int general = opts && (opts->flags & PSS_ENQ_GENERAL);
     if (!general) {
-        uint32_t max_k = 0;
-        for (uint32_t r = 0; r < rows; ++r) max_k = s->h_topk[r] > max_k ? s->h_topk[r] : max_k;
+        uint32_t max_k = 0, max_w = 0;
+        for (uint32_t r = 0; r < rows; ++r) {
+            max_k = s->h_topk[r] > max_k ? s->h_topk[r] : max_k;
+            max_w = s->h_wlen[r] > max_w ? s->h_wlen[r] : max_w;
+        }
         const hipEvent_t split = opts ? (hipEvent_t)opts->split_event : NULL;
         const uint32_t fl = opts ? opts->flags : 0u;
         const int form = (fl & PSS_ENQ_SPLIT)   ? PSS_FORM_SPLIT
                          : (fl & PSS_ENQ_FUSED) ? PSS_FORM_FUSED
                          : (fl & PSS_ENQ_SMALL) ? PSS_FORM_SMALL
                                                 : -1;
-        if (pss_stream_launch(a, rows, max_k, form, s->stream, split) != hipSuccess) return PSS_ERR_HIP;
+        if (pss_stream_launch(a, rows, max_k, max_w, form, s->stream, split) != hipSuccess) return PSS_ERR_HIP;
         return PSS_OK;
     }
     pss_general_kernel<<<dim3(rows), dim3(PSS_GEN_NT), 0, s->stream>>>(a);

@@ -39,6 +39,8 @@
 #define PSS_ROW_BITS 8192u       /* fused form: penalty-bitmap words of the general algorithm */
 #define PSS_SEG_KMAX 256u        /* largest top-k the segment kernel covers (running top-4 per lane) */
 #define PSS_SEG_WMAX 256u        /* largest window the segment kernel covers (four ids per lane) */
+#define PSS_WIDE_KMAX 1024u      /* largest top-k of the wide fused form (running top-4, 16 waves) */
+#define PSS_WIDE_LIST_CAP 8192u  /* the wide fused form's LDS candidate list */
 #define PSS_SEG_MAX_SLOTS 256u   /* items per row (V <= 262144 at items >= 1024 ids) */
 #define PSS_POOL_CAP 16384u      /* pool entries per row, split evenly over its items */
 #define PSS_FIN_LIST_CAP 4096u   /* candidates the finisher gathers in LDS */
@@ -87,12 +89,15 @@ __device__ __forceinline__ void pss_st_agent64(unsigned long long* p, unsigned l
 /* ------------------------------------------------------------------------ */
 
 /* Fused form: the workgroup's candidate list and row-level values. */
-struct pss_row_lds {
-    unsigned long long list[PSS_ROW_LIST_CAP]; /* (key << 32) | id */
-    unsigned long long best;                   /* greedy rows: (key << 32) | ~id */
-    uint32_t n;                                /* entries claimed (may exceed the capacity) */
-    uint32_t bound;                            /* largest certified bound of the row */
+template <uint32_t CAP>
+struct pss_row_lds_t {
+    static constexpr uint32_t cap = CAP;
+    unsigned long long list[CAP]; /* (key << 32) | id */
+    unsigned long long best;      /* greedy rows: (key << 32) | ~id */
+    uint32_t n;                   /* entries claimed (may exceed the capacity) */
+    uint32_t bound;               /* largest certified bound of the row */
 };
+using pss_row_lds = pss_row_lds_t<PSS_ROW_LIST_CAP>;
 
 /* Finisher scratch besides the candidate list. */
 struct pss_fin_small {
@@ -720,15 +725,17 @@ struct pss_wave_lds {
 };
 
 /* Row tests from the raw parameters (no division).  A row is covered when
- * it is greedy, or its top-k is on and at most PSS_SEG_KMAX and its window
- * at most PSS_SEG_WMAX ids; the finisher runs the general algorithm on the
+ * it is greedy, or its top-k is on and at most a.kmax_cov and its window at
+ * most a.wmax_cov ids (PSS_SEG_KMAX / PSS_SEG_WMAX, or the wide fused form's
+ * PSS_WIDE_KMAX / PSS_MAX_PENALTY_LEN); the finisher runs the general algorithm on the
  * others and the segment kernel skips them. */
 __device__ __forceinline__ bool pss_seg_row_greedy(const pss_args& a, const sample_params& sp) {
     return (a.mode == PSS_MODE_GREEDY) || !(sp.temperature > 0.0f);
 }
 __device__ __forceinline__ bool pss_seg_row_covered(const pss_args& a, const sample_params& sp) {
     const uint32_t K = sp.topK < a.V ? sp.topK : a.V;
-    return pss_seg_row_greedy(a, sp) || (K > 0u && K <= PSS_SEG_KMAX && sp.penaltyLength <= PSS_SEG_WMAX);
+    const uint32_t W = sp.penaltyLength < PSS_MAX_PENALTY_LEN ? sp.penaltyLength : PSS_MAX_PENALTY_LEN;
+    return pss_seg_row_greedy(a, sp) || (K > 0u && K <= a.kmax_cov && W <= a.wmax_cov);
 }
 
 /* Buffer resource word 3 for raw (untyped, stride 0) buffer loads on gfx9
@@ -904,11 +911,11 @@ struct pss_wave_run {
  * restrict argument: the kernel's stores cannot alias it, so the row
  * parameters of later items still come through scalar loads.
  */
-template <int EPT, int DT, bool M1, bool FUSED, bool SMALL = false>
+template <int EPT, int DT, bool M1, bool FUSED, bool SMALL = false, bool WL = false, class RL = pss_row_lds>
 __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, uint32_t i0, uint32_t i1,
                                                const sample_params* __restrict__ params,
                                                pss_wave_lds<EPT, DT>* lds, unsigned long long* joint,
-                                               pss_row_lds* rl) {
+                                               RL* rl, const uint32_t* win = nullptr) {
     using Gm = pss_wgeom<EPT, DT>;
     constexpr int E = Gm::E, NL = Gm::NL;
     constexpr uint32_t ITEM = Gm::ITEM;
@@ -978,7 +985,32 @@ __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, u
             const float invT = greedy ? 1.0f : c.invT;
             pss_wait_mem(); /* this item's staged loads and side values */
             __asm__ __volatile__("" ::: "memory");
-            if (doPen) {
+            if (WL && doPen) {
+                /* window in LDS (win[0..W), wide fused form): its ids in this
+                 * item become -inf in the staging area and claimed (their
+                 * penalized values entered the list before the rounds);
+                 * duplicates write the same values */
+                const uint32_t nh = (c.W + (uint32_t)PSS_WAVE - 1u) / (uint32_t)PSS_WAVE;
+                for (uint32_t h = 0; h < nh; ++h) {
+                    const uint32_t idx = h * (uint32_t)PSS_WAVE + lane;
+                    const uint32_t id = idx < c.W ? win[idx] : PSS_SENTINEL;
+                    const bool inr = id >= base && id - base < ITEM && id < V;
+                    if (__ballot(inr) != 0ull && inr) {
+                        const uint32_t o = id - base;
+                        const uint32_t li = o / (uint32_t)(PSS_WAVE * E), rr = o % (uint32_t)(PSS_WAVE * E);
+                        const uint32_t owner = rr / (uint32_t)E, e = rr % (uint32_t)E;
+                        atomicOr(&wl.claim[owner], 1u << (li * (uint32_t)E + e));
+                        char* p = (char*)&wl.stage[li][owner] + e * esz;
+                        if (DT == PSS_DTYPE_F16) {
+                            const uint16_t ninf = 0xFC00u;
+                            __builtin_memcpy(p, &ninf, 2);
+                        } else {
+                            *(float*)p = NEG_INF;
+                        }
+                    }
+                }
+            }
+            if (!WL && doPen) {
 #pragma unroll
                 for (int h = 0; h < 4; ++h) {
                     const uint32_t id = sd.hid[h];
@@ -1154,7 +1186,7 @@ __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, u
             auto id_of = [&](uint32_t i) -> uint32_t {
                 return base + (i / E) * (PSS_WAVE * E) + lane * E + (i % E);
             };
-            const uint32_t capw = FUSED ? PSS_ROW_LIST_CAP : pss_pool_capw(NS);
+            const uint32_t capw = FUSED ? RL::cap : pss_pool_capw(NS);
             uint32_t pm = 0u, ovp = 0u;
             bool any = true;
             if (thr <= PSS_KEY_NEG_INF) {
@@ -1228,7 +1260,7 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_seg_kernel(pss_args a, uint32_
     const uint32_t i0 = blockIdx.x * per_wg;
     const uint32_t i1 = i0 + per_wg < n_items ? i0 + per_wg : n_items;
     if (i0 >= i1) return;
-    pss_seg_rounds<EPT, DT, M1, false>(a, NS, i0, i1, params, lds, joint, nullptr);
+    pss_seg_rounds<EPT, DT, M1, false>(a, NS, i0, i1, params, lds, joint, (pss_row_lds*)nullptr);
 }
 
 /*
@@ -1246,15 +1278,28 @@ union pss_row_scratch {
         pss_fin_small f;
         uint32_t bits[PSS_ROW_BITS];
     } fin;
+    uint32_t hash[2u * PSS_MAX_PENALTY_LEN]; /* wide form: window dedup before the rounds */
 };
 
-template <int EPT, int DT, bool M1>
+/*
+ * WIDE (top-k up to PSS_WIDE_KMAX, windows up to PSS_MAX_PENALTY_LEN): the
+ * row's window goes to LDS before the rounds; each distinct id in it (an LDS
+ * hash set with linear probing, load factor <= 1/2) enters the candidate
+ * list with its penalized value, unconditionally, and the rounds turn the
+ * window's ids to -inf in their staging areas (pss_seg_rounds WL).  The list
+ * holds PSS_WIDE_LIST_CAP entries; the items are 1,024 ids (EPT 16) to make
+ * room for it, and the lanes keep a running top-4 (the certificate's
+ * ceil(K/16)-th largest of 256 values, K <= 1024).
+ */
+template <int EPT, int DT, bool M1, bool WIDE>
 __global__ void __launch_bounds__(PSS_SEG_NT) pss_row_kernel(pss_args a, uint32_t NS,
                                                              const sample_params* __restrict__ params) {
     constexpr int NT = PSS_SEG_NT;
+    using RL = pss_row_lds_t<WIDE ? PSS_WIDE_LIST_CAP : PSS_ROW_LIST_CAP>;
     __shared__ pss_row_scratch<EPT, DT> U;
     __shared__ unsigned long long joint[PSS_SEG_NW];
-    __shared__ pss_row_lds rl;
+    __shared__ RL rl;
+    __shared__ uint32_t win[WIDE ? PSS_MAX_PENALTY_LEN : 1];
     pss_globalize(a);
     const uint32_t row = blockIdx.x, tid = pss_tid();
     const sample_params sp = params[row];
@@ -1268,15 +1313,46 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_row_kernel(pss_args a, uint32_
         rl.best = 0ull;
     }
     const bool covered = pss_seg_row_covered(a, sp);
-    if (covered) pss_seg_rounds<EPT, DT, M1, true>(a, NS, row * NS, row * NS + NS, params, U.st, joint, &rl);
-    __syncthreads();
     const pss_rowcfg c = pss_make_rowcfg(sp, a.V);
+    if (WIDE && covered && !pss_seg_row_greedy(a, sp) && c.doPen) {
+        static_assert(PSS_MAX_PENALTY_LEN <= PSS_SEG_NT, "one window id per thread");
+        const uint32_t* hist_row = a.history + (size_t)row * PSS_MAX_PENALTY_LEN;
+        for (uint32_t i = tid; i < 2u * PSS_MAX_PENALTY_LEN; i += NT) U.hash[i] = PSS_SENTINEL;
+        const uint32_t id = tid < c.W ? hist_row[tid] : PSS_SENTINEL;
+        if (tid < c.W) win[tid] = id;
+        __syncthreads();
+        if (id < a.V) {
+            uint32_t h = (id * 2654435761u) >> 21; /* 11 bits: 2,048 slots */
+            bool owner = false;
+            for (uint32_t probe = 0; probe < 2u * PSS_MAX_PENALTY_LEN; ++probe) {
+                const uint32_t old = atomicCAS(&U.hash[h], PSS_SENTINEL, id);
+                if (old == PSS_SENTINEL) {
+                    owner = true;
+                    break;
+                }
+                if (old == id) break;
+                h = (h + 1u) & (2u * PSS_MAX_PENALTY_LEN - 1u);
+            }
+            if (owner) {
+                const char* rowp = (const char*)a.logits + (size_t)row * a.stride * (DT == PSS_DTYPE_F16 ? 2u : 4u);
+                const float x = pss_load1(rowp, DT, id);
+                const float pen = pss_penalize(x * c.invT, c);
+                const uint32_t pos = atomicAdd(&rl.n, 1u);
+                if (pos < RL::cap) rl.list[pos] = ((unsigned long long)pss_key(pss_canon(pen)) << 32) | id;
+            }
+        }
+        __syncthreads(); /* the hash shares the staging area */
+    }
+    if (covered)
+        pss_seg_rounds<EPT, DT, M1, true, false, WIDE, RL>(a, NS, row * NS, row * NS + NS, params, U.st, joint, &rl,
+                                                          win);
+    __syncthreads();
     if (pss_seg_row_greedy(a, sp)) {
         pss_greedy_finish<NT>(a, row, rl.best);
         return;
     }
     const uint32_t n = rl.n;
-    bool general = !covered || n > PSS_ROW_LIST_CAP;
+    bool general = !covered || n > RL::cap;
     if (!general && !pss_list_finish_fast<NT>(a, row, c, rl.list, n, rl.bound, pre, U.fin.f))
         pss_list_finish<NT>(a, row, c, rl.list, n, U.fin.f.g, rl.bound);
     if (general) pss_general_row<NT>(a, row, U.fin.f.g, U.fin.bits, PSS_ROW_BITS);
@@ -1461,7 +1537,7 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_small_kernel(pss_args a, uint3
     const uint32_t row = blockIdx.x / GW, g = blockIdx.x - row * GW;
     const uint32_t s0 = g * NS / GW, s1 = (g + 1u) * NS / GW;
     const uint32_t tid = pss_tid();
-    pss_seg_rounds<EPT, DT, M1, false, true>(a, NS, row * NS + s0, row * NS + s1, params, U.st, joint, nullptr);
+    pss_seg_rounds<EPT, DT, M1, false, true>(a, NS, row * NS + s0, row * NS + s1, params, U.st, joint, (pss_row_lds*)nullptr);
     pss_wait_mem(); /* this wave's pool stores, counts and staged loads have completed */
     __syncthreads();
     if (tid == 0u) {
@@ -1559,14 +1635,14 @@ static inline hipError_t pss_stream_go(const pss_args& a, uint32_t rows, uint32_
         const dim3 grid(rows), block(PSS_SEG_NT);
         if (a.dtype == PSS_DTYPE_F16) {
             if (m1)
-                pss_row_kernel<EPT, PSS_DTYPE_F16, true><<<grid, block, 0, st>>>(a, NS, a.params);
+                pss_row_kernel<EPT, PSS_DTYPE_F16, true, false><<<grid, block, 0, st>>>(a, NS, a.params);
             else
-                pss_row_kernel<EPT, PSS_DTYPE_F16, false><<<grid, block, 0, st>>>(a, NS, a.params);
+                pss_row_kernel<EPT, PSS_DTYPE_F16, false, false><<<grid, block, 0, st>>>(a, NS, a.params);
         } else {
             if (m1)
-                pss_row_kernel<EPT, PSS_DTYPE_F32, true><<<grid, block, 0, st>>>(a, NS, a.params);
+                pss_row_kernel<EPT, PSS_DTYPE_F32, true, false><<<grid, block, 0, st>>>(a, NS, a.params);
             else
-                pss_row_kernel<EPT, PSS_DTYPE_F32, false><<<grid, block, 0, st>>>(a, NS, a.params);
+                pss_row_kernel<EPT, PSS_DTYPE_F32, false, false><<<grid, block, 0, st>>>(a, NS, a.params);
         }
         if ((e = hipGetLastError()) != hipSuccess) return e;
         if (split_ev && (e = hipEventRecord(split_ev, st)) != hipSuccess) return e;
@@ -1602,15 +1678,32 @@ static inline uint32_t pss_small_capacity() {
     return cap;
 }
 
-/* max_k: the largest top-k of the launched rows (an upper bound is enough).
- * form: PSS_FORM_*, or -1 to choose: the small-batch form while its grid is
- * at most one pass of resident workgroups (every row spread over several CUs,
- * one round), the fused form above that.  All forms compute the same bits. */
-static inline hipError_t pss_stream_launch(pss_args a, uint32_t rows, uint32_t max_k, int form,
+/* max_k, max_w: the largest top-k and window of the launched rows (upper
+ * bounds are enough).  form: PSS_FORM_*, or -1 to choose: the small-batch
+ * form while its grid is at most one pass of resident workgroups (every row
+ * spread over several CUs, one round), the fused form above that; rows with a
+ * top-k above PSS_SEG_KMAX or a window above PSS_SEG_WMAX take the wide fused
+ * form (unless a split or small-batch form is forced, which leaves them to
+ * the general algorithm).  All forms compute the same bits. */
+static inline hipError_t pss_stream_launch(pss_args a, uint32_t rows, uint32_t max_k, uint32_t max_w, int form,
                                            hipStream_t st, hipEvent_t split_ev) {
     const size_t esz = a.dtype == PSS_DTYPE_F16 ? 2u : 4u;
     a.vec_ok = ((a.stride * esz) % 16u == 0u) && (((uintptr_t)a.logits & 15u) == 0u) &&
                ((a.V * esz) % 16u == 0u);
+    if ((max_k > PSS_SEG_KMAX || max_w > PSS_SEG_WMAX) && (form < 0 || form == PSS_FORM_FUSED)) {
+        const uint32_t NS = (a.V + (uint32_t)PSS_WAVE * 16u - 1u) / ((uint32_t)PSS_WAVE * 16u);
+        if (NS > PSS_SEG_MAX_SLOTS) return hipErrorInvalidValue;
+        a.kmax_cov = PSS_WIDE_KMAX;
+        a.wmax_cov = PSS_MAX_PENALTY_LEN;
+        const dim3 grid(rows), block(PSS_SEG_NT);
+        if (a.dtype == PSS_DTYPE_F16)
+            pss_row_kernel<16, PSS_DTYPE_F16, false, true><<<grid, block, 0, st>>>(a, NS, a.params);
+        else
+            pss_row_kernel<16, PSS_DTYPE_F32, false, true><<<grid, block, 0, st>>>(a, NS, a.params);
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess && split_ev) e = hipEventRecord(split_ev, st);
+        return e;
+    }
     const int ept = pss_stream_pick_ept(a.V, rows);
     if (form < 0) {
         const uint64_t item = (uint64_t)PSS_WAVE * ept;

@@ -93,6 +93,45 @@ def test_c5_adversarial(flags):
              where="c5")
 
 
+WIDE_CASES = {
+    # name: (V, dtype, topK, W, window kind)
+    "k300_w512_uniform": (102400, np.float32, 300, 512, "uniform"),
+    "k1024_w1024_dups": (102400, np.float32, 1024, 1024, "dups"),
+    "k700_w300_clustered": (248320, np.float32, 700, 300, "clustered"),
+    "k257_w1024_f16": (65536, np.float16, 257, 1024, "uniform"),
+    "k40_w600": (102400, np.float32, 40, 600, "uniform"),
+    "k1000_small_vocab": (4000, np.float32, 1000, 64, "uniform"),
+}
+
+
+@pytest.mark.parametrize("flags", [0, S.ENQ_FUSED], ids=["auto", "fused"])
+@pytest.mark.parametrize("case", sorted(WIDE_CASES))
+def test_wide_fused(case, flags):
+    """The wide fused form (top-k up to 1,024, windows up to 1,024 in LDS):
+    duplicate window ids, ids at or beyond V, a window clustered in a few
+    items, fp16, and a vocabulary too small for the joint certificate (the
+    list then takes every element, or the row goes to the general algorithm);
+    chained over two steps so the window ring advances."""
+    V, dt, K, W, kind = WIDE_CASES[case]
+    rng = np.random.default_rng(sum(case.encode()))
+    rows = 5
+    logits = rng.normal(0.0, 3.0, (rows, V)).astype(dt)
+    params = O.make_params(temperature=0.9, repPenalty=1.2, presencePenalty=0.3, penaltyLength=W, topK=K,
+                           topP=0.97, minP=0.01, rows=rows)
+    hist = O.new_history(rows)
+    for r in range(rows):
+        if kind == "uniform":
+            ids = rng.integers(0, V, W)
+        elif kind == "dups":
+            ids = rng.integers(0, 300, W)            # many duplicates
+            ids[::7] = V + rng.integers(0, 5, ids[::7].size)  # ids beyond the vocab
+        else:
+            ids = rng.integers(0, 2048, W) + 4096 * (r + 1)   # one or two items
+        hist[r, :W] = ids.astype(np.uint32)
+    run_both(logits, params, np.arange(1, rows + 1, dtype=np.uint32), hist, None, flags=flags, steps=2,
+             step_logits=[logits, np.roll(logits, 3, axis=1)], where=f"wide {case}")
+
+
 FULL_BATCHES = {
     # name: (generator, rows) -- row counts that select each fast-kernel shape
     "headline_256x102400_f32": (lambda: WL.headline(seed=31), None),   # 512 x 200, one segment
