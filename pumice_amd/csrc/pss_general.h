@@ -127,6 +127,27 @@ struct pss_gen_shared {
     uint32_t tok;
 };
 
+/* hist[d] += w for every lane with w != 0 (all 64 lanes active): the lanes
+ * sharing the first pending lane's digit combine into one atomic (their count
+ * when `unit`, else a wave sum), up to four digits while each covers at least
+ * 8 lanes; the rest add one by one.  With heavy ties a wave's lanes share one
+ * or two digits; with spread keys the plain atomics are cheaper. */
+__device__ __forceinline__ void pss_hist_add_wave(uint64_t* hist, uint32_t d, uint64_t w, bool unit) {
+    const uint32_t lane = pss_tid() & 63u;
+    uint64_t pending = __ballot(w != 0ull);
+    for (int it = 0; it < 4 && pending; ++it) {
+        const uint32_t leader = (uint32_t)__builtin_ctzll(pending);
+        const uint32_t dl = __builtin_amdgcn_readlane(d, leader);
+        const bool in = ((pending >> lane) & 1ull) && d == dl;
+        const uint64_t m = __ballot(in);
+        if (__popcll(m) < 8) break;
+        const uint64_t tot = unit ? (uint64_t)__popcll(m) : wave_sum_u64(in ? w : 0ull);
+        if (lane == leader) atomicAdd((unsigned long long*)&hist[dl], (unsigned long long)tot);
+        pending &= ~m;
+    }
+    if ((pending >> lane) & 1ull) atomicAdd((unsigned long long*)&hist[d], (unsigned long long)w);
+}
+
 template <int NT>
 __device__ __forceinline__ void pss_general_row(const pss_args& a, uint32_t row, pss_gen_shared& sh, uint32_t* bits,
                                 uint32_t bit_words) {
@@ -193,22 +214,36 @@ __device__ __forceinline__ void pss_general_row(const pss_args& a, uint32_t row,
     const float tmax = pss_unkey(tmaxKey);
 
     /* Radix select over the row: digit levels of 8 bits from the top.  weight
-     * 0 = count (top-k), 1 = mass restricted to key >= lo (top-p). */
+     * 0 = count (top-k), 1 = mass restricted to key >= lo (top-p).  Without
+     * chunking every lane runs every iteration (ids past V weigh nothing), so
+     * the wave can combine its lanes' additions per digit (pss_hist_add_wave:
+     * tied values put a whole wave on one bin, where separate LDS atomics to
+     * one address serialize). */
     auto select = [&](uint64_t rem, int weight, uint32_t lo) -> uint32_t {
         uint32_t prefix = 0, pmask = 0;
         for (int shift = 24; shift >= 0; shift -= 8) {
             for (uint32_t i = tid; i < 256u; i += NT) sh.hist[i] = 0;
             __syncthreads();
-            pass([&](uint32_t, float t) {
-                const uint32_t k = pss_key(t);
-                if ((k & pmask) != prefix) return;
-                if (weight == 0) {
-                    atomicAdd((unsigned long long*)&sh.hist[(k >> shift) & 255u], 1ull);
-                } else if (k >= lo) {
-                    const uint64_t q = pss_fixq(pss_prob(t, tmax));
-                    if (q) atomicAdd((unsigned long long*)&sh.hist[(k >> shift) & 255u], (unsigned long long)q);
+            auto wof = [&](float t, uint32_t k) -> uint64_t {
+                if ((k & pmask) != prefix) return 0ull;
+                if (weight == 0) return 1ull;
+                return k >= lo ? pss_fixq(pss_prob(t, tmax)) : 0ull;
+            };
+            if (!chunked) {
+                for (uint32_t j0 = 0; j0 < V; j0 += NT) {
+                    const uint32_t j = j0 + tid;
+                    const float t = j < V ? T(j, 0u) : pss_u2f(0xFF800000u);
+                    const uint32_t k = pss_key(t);
+                    const uint64_t w = j < V ? wof(t, k) : 0ull;
+                    pss_hist_add_wave(sh.hist, (k >> shift) & 255u, w, weight == 0);
                 }
-            });
+            } else {
+                pass([&](uint32_t, float t) {
+                    const uint32_t k = pss_key(t);
+                    const uint64_t w = wof(t, k);
+                    if (w) atomicAdd((unsigned long long*)&sh.hist[(k >> shift) & 255u], (unsigned long long)w);
+                });
+            }
             __syncthreads();
             if (tid < 64) wave0_pick_digit(sh.hist, rem, &sh.digit, &sh.rem);
             __syncthreads();
