@@ -127,6 +127,13 @@ struct pss_gen_shared {
     uint32_t tok;
 };
 
+/* First digit shift of a select over keys in [lo, hi]: below their common
+ * prefix; -1 when lo == hi. */
+__device__ __forceinline__ int pss_gen_select_shift(uint32_t lo, uint32_t hi) {
+    const uint32_t d = lo ^ hi;
+    return d ? ((31 - (int)__clz(d)) / 8) * 8 : -1;
+}
+
 /* hist[d] += w for every lane with w != 0 (all 64 lanes active): the lanes
  * sharing the first pending lane's digit combine into one atomic (their count
  * when `unit`, else a wave sum), up to four digits while each covers at least
@@ -204,13 +211,16 @@ __device__ __forceinline__ void pss_general_row(const pss_args& a, uint32_t row,
         }
     };
 
-    /* S3 */
-    uint64_t mk = 0;
+    /* S3, and the smallest key: the radix selects start below the common
+     * prefix of the range they search (none at all on an all-equal row) */
+    uint64_t mk = 0, nk = 0;
     pass([&](uint32_t, float t) {
         const uint64_t k = pss_key(t);
         mk = k > mk ? k : mk;
+        nk = (0xFFFFFFFFull ^ k) > nk ? (0xFFFFFFFFull ^ k) : nk;
     });
     const uint32_t tmaxKey = (uint32_t)block_max_u64<NT>(mk, sh.red);
+    const uint32_t tminKey = (uint32_t)(0xFFFFFFFFull ^ block_max_u64<NT>(nk, sh.red));
     const float tmax = pss_unkey(tmaxKey);
 
     /* Radix select over the row: digit levels of 8 bits from the top.  weight
@@ -220,8 +230,12 @@ __device__ __forceinline__ void pss_general_row(const pss_args& a, uint32_t row,
      * tied values put a whole wave on one bin, where separate LDS atomics to
      * one address serialize). */
     auto select = [&](uint64_t rem, int weight, uint32_t lo) -> uint32_t {
-        uint32_t prefix = 0, pmask = 0;
-        for (int shift = 24; shift >= 0; shift -= 8) {
+        /* every weighted key lies in [max(lo, tminKey), tmaxKey] */
+        const int top = pss_gen_select_shift(lo > tminKey ? lo : tminKey, tmaxKey);
+        if (top < 0) return tmaxKey;
+        uint32_t pmask = top + 8 >= 32 ? 0u : ~((1u << (top + 8)) - 1u);
+        uint32_t prefix = tmaxKey & pmask;
+        for (int shift = top; shift >= 0; shift -= 8) {
             for (uint32_t i = tid; i < 256u; i += NT) sh.hist[i] = 0;
             __syncthreads();
             auto wof = [&](float t, uint32_t k) -> uint64_t {
