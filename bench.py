@@ -15,6 +15,9 @@ A "step" is one pss_enqueue over a batch of logit rows resident in HBM.
             into pinned host memory), per-step GPU time, and steady
             decode-group us/token through the C generate loop.
   c3/c4/c5  the other batched configurations, rows/s and GB/s.
+  lmhead    the LM head before the sampler (RMSNorm + fp16 GEMV over a
+            4,096 x 102,400 block-transposed head): us per call and HBM GB/s
+            for 1 and 4 rows, logits and fused-greedy forms.
   cpu_baseline  the O1 oracle (scalar C, sort-based) on the box's host cores
             over a bounded sample of the headline rows.
 
@@ -179,6 +182,51 @@ def bench_latency(steps):
                 decode_group_tokens_agree=bool(toks_gen == toks_pin))
 
 
+def bench_lmhead(steps, K=4096, V=102400, rows_list=(1, 4)):
+    """LM head (RMSNorm + fp16 GEMV, K x V block-transposed head): us per call
+    of plh_logits and plh_greedy, back-to-back on the head's stream, and the
+    algorithmic HBM rate (K V 2 head bytes + rows (2 K + V) 4 per call)."""
+    from pumice_amd import hip
+    from pumice_amd import lmhead as L
+    from pumice_amd import sampler as S
+
+    rng = np.random.default_rng(0)
+    w = rng.integers(0x2000, 0x3C00, (K // 8, V, 8), dtype=np.uint16) | \
+        (rng.integers(0, 2, (K // 8, V, 8), dtype=np.uint16) << 15)
+    rmax = max(rows_list)
+    x = rng.normal(0, 2, (rmax, K)).astype(np.float32)
+    g = rng.normal(1, 0.2, K).astype(np.float32)
+    dw, dg, dx = hip.DeviceBuffer.from_array(w), hip.DeviceBuffer.from_array(g), hip.DeviceBuffer.from_array(x)
+    del w
+    dl = hip.DeviceBuffer(rmax * V * 4)
+    head = L.LMHead(dw.ptr, dg.ptr, K, V, rmax)
+    s = S.Sampler(V, rmax, stream=head.stream)
+    out = {"K": K, "V": V, "head_bytes": K * V * 2}
+    try:
+        for rows in rows_list:
+            nbytes = K * V * 2 + rows * (2 * K + V) * 4
+            for name, call in [("logits", lambda: head.logits(dx.ptr, K, rows, dl.ptr, V)),
+                               ("greedy", lambda: head.greedy(s, dx.ptr, K, rows, do_increment=0))]:
+                for _ in range(3):
+                    call()
+                e0, e1 = hip.Event(), hip.Event()
+                e0.record(head.stream)
+                for _ in range(steps):
+                    call()
+                e1.record(head.stream)
+                hip.stream_sync(head.stream)
+                us = e0.elapsed_ms(e1) * 1e3 / steps
+                out[f"{name}_rows{rows}_us"] = us
+                out[f"{name}_rows{rows}_gbps"] = nbytes / (us * 1e-6) / 1e9
+        out["logits_rows1_frac"] = out["logits_rows1_gbps"] / HBM_PEAK_GBPS
+    finally:
+        s.close()
+        head.close()
+        for b in (dw, dg, dx, dl):
+            b.free()
+    return out
+
+
 def cpu_baseline(w, seconds):
     """O1 (scalar C, sort-based restatement) on a bounded sample of the headline rows."""
     import oracle as O
@@ -294,6 +342,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="headline only (c3/c4/c5 and latency skipped)")
     ap.add_argument("--latency-only", action="store_true",
                     help="only the batch-1 latency section (for kernel traces of the small-batch form)")
+    ap.add_argument("--lmhead-only", action="store_true",
+                    help="only the LM-head section (for kernel traces of plh_gemv_kernel)")
+    ap.add_argument("--lmhead-steps", type=int, default=50)
     ap.add_argument("--general", action="store_true", help="force the general kernel")
     ap.add_argument("--split", action="store_true", help="force the two-kernel form")
     ap.add_argument("--copy-calib", action="store_true",
@@ -314,6 +365,10 @@ def main():
     from pumice_amd import sampler as S
     from pumice_amd import workloads as WL
 
+    if args.lmhead_only:
+        log("lm head (K 4096 x V 102400)")
+        print(json.dumps({"lmhead": bench_lmhead(args.lmhead_steps)}), flush=True)
+        return
     if args.latency_only:
         log("latency (batch 1)")
         lat = bench_latency(args.latency_steps)
@@ -339,6 +394,9 @@ def main():
         log("latency (batch 1)")
         extra["latency_b1"] = bench_latency(args.latency_steps)
         log("latency", json.dumps(extra["latency_b1"]))
+        log("lm head (K 4096 x V 102400)")
+        extra["lmhead"] = bench_lmhead(args.lmhead_steps)
+        log("lmhead", json.dumps(extra["lmhead"]))
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")

@@ -106,6 +106,20 @@ def lib():
         L.oracle_o1_score_row.argtypes = [P, u32, u32, P, P]
         L.oracle_log64.restype = ctypes.c_double
         L.oracle_log64.argtypes = [ctypes.c_double]
+        L.oracle_float_to_fp16_many.restype = None
+        L.oracle_float_to_fp16_many.argtypes = [P, P, u64]
+        L.oracle_fp16_to_float_many.restype = None
+        L.oracle_fp16_to_float_many.argtypes = [P, P, u64]
+        L.oracle_get_data_fp16.restype = None
+        L.oracle_get_data_fp16.argtypes = [i32, i32, i32, P]
+        L.oracle_transpose_block16_fp16.restype = None
+        L.oracle_transpose_block16_fp16.argtypes = [P, P, u32, u32]
+        L.oracle_lmhead_norm.restype = f32
+        L.oracle_lmhead_norm.argtypes = [P, P, u32, P]
+        L.oracle_lmhead_logits.restype = None
+        L.oracle_lmhead_logits.argtypes = [P, P, u32, u32, u32, P]
+        L.oracle_lmhead_logits64.restype = None
+        L.oracle_lmhead_logits64.argtypes = [P, P, u32, u32, P, P]
         _lib = L
     return _lib
 
@@ -241,6 +255,67 @@ def get_data(seed, M, N):
     out = np.zeros((M, N), np.float32)
     lib().oracle_get_data(seed, M, N, _ptr(out))
     return out
+
+
+def float_to_fp16(f):
+    """src/data.c:30-52 (truncating) over an array; returns uint16 bits."""
+    f = np.ascontiguousarray(f, np.float32)
+    h = np.zeros(f.shape, np.uint16)
+    lib().oracle_float_to_fp16_many(_ptr(f), _ptr(h), f.size)
+    return h
+
+
+def fp16_to_float(h):
+    h = np.ascontiguousarray(h, np.uint16)
+    f = np.zeros(h.shape, np.float32)
+    lib().oracle_fp16_to_float_many(_ptr(h), _ptr(f), h.size)
+    return f
+
+
+def get_data_fp16(seed, M, N):
+    """src/data.c:83-93 getDataFP16: uint16 bits [M][N]."""
+    out = np.zeros((M, N), np.uint16)
+    lib().oracle_get_data_fp16(seed, M, N, _ptr(out))
+    return out
+
+
+def transpose_block16(w_kv):
+    """src/data.c:305-331 (FP16): [K][V] -> [K/8][V][8]."""
+    w = np.ascontiguousarray(w_kv, np.uint16)
+    K, V = w.shape
+    out = np.zeros((K // 8, V, 8), np.uint16)
+    lib().oracle_transpose_block16_fp16(_ptr(w), _ptr(out), K, V)
+    return out
+
+
+def lmhead_norm(x, gamma):
+    """RMSNorm of LMHead-GEMV-Q16.comp:34-58 in the GPU's order: (inv_rms, a)."""
+    x = np.ascontiguousarray(x, np.float32)
+    g = np.ascontiguousarray(gamma, np.float32)
+    a = np.zeros(x.size, np.float32)
+    inv = lib().oracle_lmhead_norm(_ptr(x), _ptr(g), x.size, _ptr(a))
+    return float(np.float32(inv)), a
+
+
+def lmhead_logits(a, w_bt, slices=4):
+    """GEMV of LMHead-GEMV-Q16.comp:60-70 in the GPU's K-slice order (fp32)."""
+    a = np.ascontiguousarray(a, np.float32)
+    w = np.ascontiguousarray(w_bt, np.uint16)
+    KB, V, _ = w.shape
+    out = np.zeros(V, np.float32)
+    lib().oracle_lmhead_logits(_ptr(a), _ptr(w), 8 * KB, V, slices, _ptr(out))
+    return out
+
+
+def lmhead_logits64(a, w_bt):
+    """The same GEMV in binary64, with sum |a w| per column."""
+    a = np.ascontiguousarray(a, np.float32)
+    w = np.ascontiguousarray(w_bt, np.uint16)
+    KB, V, _ = w.shape
+    out = np.zeros(V, np.float64)
+    absdot = np.zeros(V, np.float64)
+    lib().oracle_lmhead_logits64(_ptr(a), _ptr(w), 8 * KB, V, _ptr(out), _ptr(absdot))
+    return out, absdot
 
 
 def exp_many(x):

@@ -17,6 +17,8 @@
  * greedy                    LMHead-GEMV-ArgMax-Q16.comp:75-96 +
  *                           ArgMax-Reduce.comp:135-167.
  * get_pseudo_random         src/data.c:8-28.
+ * fp16 data, LM head        src/data.c:30-93, :305-331; LMHead-GEMV-Q16.comp:28-72
+ *                           in the GPU's summation order (plh_lmhead.hip).
  *
  * Built with -ffp-contract=off; pss_exp and the integer helpers come from the
  * shared deterministic math header, pinned by tests against libm and
@@ -728,6 +730,133 @@ float oracle_get_pseudo_random(int i, int j, int seed) {
 void oracle_get_data(int seed, int M, int N, float* out) {
     for (int i = 0; i < M; ++i)
         for (int j = 0; j < N; ++j) out[(size_t)i * N + j] = oracle_get_pseudo_random(i, j, seed);
+}
+
+/* ------------------------------------------------------------------------ */
+/* fp16 data and the LM head                                                */
+/* ------------------------------------------------------------------------ */
+
+/* src/data.c:30-52: sign, then the binary32 exponent e: e < -24 -> signed
+ * zero, e <= -15 -> subnormal with the mantissa (hidden bit included) shifted
+ * right by -1 - e, e >= 16 -> signed infinity, else the exponent rebiased
+ * and the mantissa truncated to 10 bits.  No rounding anywhere. */
+uint16_t oracle_float_to_fp16(float f) {
+    uint32_t b;
+    memcpy(&b, &f, 4);
+    const uint16_t sign = (uint16_t)((b >> 16) & 0x8000u);
+    const int e = (int)((b >> 23) & 0xFFu) - 127;
+    const uint32_t m = b & 0x7FFFFFu;
+    if (e < -24) return sign;
+    if (e <= -15) return (uint16_t)(sign | ((m | 0x800000u) >> (-1 - e)));
+    if (e >= 16) return (uint16_t)(sign | 0x7C00u);
+    return (uint16_t)(sign | ((uint32_t)(e + 15) << 10) | (m >> 13));
+}
+
+/* IEEE binary16 -> binary32 (exact): value = (-1)^s 2^(E-15) (1 + m/1024),
+ * subnormals m 2^-24, E = 31 infinities / NaNs (payload kept). */
+float oracle_fp16_to_float(uint16_t h) {
+    const uint32_t s = (uint32_t)(h & 0x8000u) << 16, E = (h >> 10) & 31u, m = h & 1023u;
+    uint32_t b;
+    if (E == 31u) {
+        b = s | 0x7F800000u | (m << 13);
+    } else if (E == 0u) {
+        const float v = ldexpf((float)m, -24);
+        memcpy(&b, &v, 4);
+        b |= s;
+    } else {
+        b = s | ((E + 112u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
+void oracle_float_to_fp16_many(const float* f, uint16_t* h, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) h[i] = oracle_float_to_fp16(f[i]);
+}
+
+void oracle_fp16_to_float_many(const uint16_t* h, float* f, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) f[i] = oracle_fp16_to_float(h[i]);
+}
+
+void oracle_get_data_fp16(int seed, int M, int N, uint16_t* out) {
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < N; ++j)
+            out[(size_t)i * N + j] = oracle_float_to_fp16(oracle_get_pseudo_random(i, j, seed));
+}
+
+/* src/data.c:305-331 with 16-bit data: output block (kb, n) = the 8 halves
+ * w[8 kb + j][n], j = 0..7, at halves offset (kb V + n) 8 + j. */
+void oracle_transpose_block16_fp16(const uint16_t* w_kv, uint16_t* w_bt, uint32_t K, uint32_t V) {
+    for (uint32_t kb = 0; kb < K / 8u; ++kb)
+        for (uint32_t n = 0; n < V; ++n)
+            for (uint32_t j = 0; j < 8u; ++j)
+                w_bt[((size_t)kb * V + n) * 8u + j] = w_kv[(size_t)(8u * kb + j) * V + n];
+}
+
+/* RMSNorm of LMHead-GEMV-Q16.comp:34-58 (src/validation.c:157-163 on the
+ * CPU): rms = sqrt(sum x^2 / K + 1e-6), a = x gamma / rms.  The sum of squares
+ * in the GPU's order: 256 strided binary64 partials (thread t: k = t, t + 256,
+ * ...), a xor butterfly over each group of 64, the four group sums in order;
+ * then binary32 for the rest, as the shader. */
+float oracle_lmhead_norm(const float* x, const float* gamma, uint32_t K, float* a) {
+    double p[256];
+    for (uint32_t t = 0; t < 256u; ++t) {
+        double s = 0.0;
+        for (uint32_t k = t; k < K; k += 256u) {
+            const double v = (double)x[k];
+            s = s + v * v;
+        }
+        p[t] = s;
+    }
+    for (uint32_t w = 0; w < 4u; ++w) {
+        double* q = p + 64u * w;
+        for (uint32_t off = 32u; off >= 1u; off >>= 1) {
+            double nq[64];
+            for (uint32_t l = 0; l < 64u; ++l) nq[l] = q[l] + q[l ^ off];
+            memcpy(q, nq, sizeof(nq));
+        }
+    }
+    double tot = p[0];
+    for (uint32_t w = 1; w < 4u; ++w) tot = tot + p[64u * w];
+    const float inv = 1.0f / sqrtf((float)tot / (float)K + 1e-6f);
+    for (uint32_t k = 0; k < K; ++k) a[k] = (x[k] * gamma[k]) * inv;
+    return inv;
+}
+
+/* The GEMV of LMHead-GEMV-Q16.comp:60-70 (acc += a[k] w[k][n] over k) in the
+ * GPU's order: slice s covers the 8-row blocks [s KB / S, (s + 1) KB / S),
+ * KB = K / 8, each an fmaf chain from 0 in ascending k; the slice partials
+ * are added in slice order. */
+void oracle_lmhead_logits(const float* a, const uint16_t* w_bt, uint32_t K, uint32_t V, uint32_t nslices,
+                          float* out) {
+    const uint32_t KB = K / 8u;
+    for (uint32_t n = 0; n < V; ++n) {
+        float tot = 0.0f;
+        for (uint32_t s = 0; s < nslices; ++s) {
+            float acc = 0.0f;
+            for (uint32_t kb = s * KB / nslices; kb < (s + 1u) * KB / nslices; ++kb) {
+                const uint16_t* blk = w_bt + ((size_t)kb * V + n) * 8u;
+                for (uint32_t j = 0; j < 8u; ++j) acc = fmaf(a[8u * kb + j], oracle_fp16_to_float(blk[j]), acc);
+            }
+            tot = s == 0u ? acc : tot + acc;
+        }
+        out[n] = tot;
+    }
+}
+
+void oracle_lmhead_logits64(const float* a, const uint16_t* w_bt, uint32_t K, uint32_t V, double* out,
+                            double* absdot) {
+    for (uint32_t n = 0; n < V; ++n) {
+        double s = 0.0, m = 0.0;
+        for (uint32_t k = 0; k < K; ++k) {
+            const double t = (double)a[k] * (double)oracle_fp16_to_float(w_bt[((size_t)(k / 8u) * V + n) * 8u + k % 8u]);
+            s += t;
+            m += fabs(t);
+        }
+        out[n] = s;
+        if (absdot) absdot[n] = m;
+    }
 }
 
 /* ------------------------------------------------------------------------ */

@@ -63,6 +63,26 @@ uint32_t oracle_greedy_two_stage(const float* logits, uint32_t V);
 float oracle_get_pseudo_random(int i, int j, int seed);
 void oracle_get_data(int seed, int M, int N, float* out);
 
+/* src/data.c:30-52 float_to_fp16 (truncating), :54-81 fp16_to_float,
+ * :83-93 getDataFP16. */
+uint16_t oracle_float_to_fp16(float f);
+float oracle_fp16_to_float(uint16_t h);
+void oracle_get_data_fp16(int seed, int M, int N, uint16_t* out);
+void oracle_float_to_fp16_many(const float* f, uint16_t* h, uint64_t n);
+void oracle_fp16_to_float_many(const uint16_t* h, float* f, uint64_t n);
+
+/* LM head (LMHead-GEMV-Q16.comp:28-72): src/data.c:305-331 transpose_block16
+ * for FP16; the RMSNorm with the GPU's summation order (returns inv_rms,
+ * writes a[K]); the GEMV over the block-transposed head with the GPU's
+ * K-slice order (nslices slices, fmaf chains, partials added in slice order);
+ * and the same GEMV in binary64 with sum |a w| for error bounds. */
+void oracle_transpose_block16_fp16(const uint16_t* w_kv, uint16_t* w_bt, uint32_t K, uint32_t V);
+float oracle_lmhead_norm(const float* x, const float* gamma, uint32_t K, float* a);
+void oracle_lmhead_logits(const float* a, const uint16_t* w_bt, uint32_t K, uint32_t V, uint32_t nslices,
+                          float* out);
+void oracle_lmhead_logits64(const float* a, const uint16_t* w_bt, uint32_t K, uint32_t V, double* out,
+                            double* absdot);
+
 /* exp checks over every binary32 x in [lo, hi], hi <= 0.  Returns the number of
  * monotonicity violations (pss_exp(x') > pss_exp(x) for x' < x); writes the max
  * error, in ulps of the exact result, against the fp64 libm exp, sampled at every

@@ -1,4 +1,5 @@
-"""Build recipe of the gfx950 sampler library (pumice_amd/libpumice_sampler.so).
+"""Build recipe of the gfx950 sampler library (pumice_amd/libpumice_sampler.so:
+the sampler and the LM head).
 
 hipcc cross-compiles for gfx950 without a GPU.  Flags:
   -ffp-contract=off                        no fused multiply-add except where the
@@ -19,7 +20,7 @@ INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "libpumice_sampler.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-HIP_SOURCES = ["pss_sampler.hip"]
+HIP_SOURCES = ["pss_sampler.hip", "plh_lmhead.hip"]
 C_SOURCES = ["pss_generate.c"]
 HIP_FLAGS = [
     "--offload-arch=gfx950",

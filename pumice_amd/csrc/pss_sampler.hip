@@ -15,27 +15,8 @@
 #include "pss_general.h"
 #include "pss_score.h"
 #include "pss_stream.h"
+#include "pss_sampler_priv.h"
 #include "pumice_sampler.h"
-
-struct pss_sampler {
-    int device;
-    hipStream_t stream;
-    int own_stream;
-    uint32_t V;
-    uint32_t max_rows;
-    sample_params* d_params;
-    uint32_t* d_rng;
-    uint32_t* d_step;
-    uint32_t* d_pos;
-    uint32_t* d_hist;
-    uint32_t* d_result;
-    uint32_t* d_tokens;
-    uint32_t* d_targets; /* scoring targets [max_rows][PSS_RESULT_SLOTS] */
-    void* d_ws;       /* streaming-kernel workspace: per-row bounds and candidate pools */
-    size_t ws_bytes;
-    uint32_t* h_topk; /* host copy of each row's topK (picks the kernel variant) */
-    uint32_t* h_wlen; /* host copy of each row's penaltyLength (likewise) */
-};
 
 #define HIP_TRY(expr)                            \
     do {                                         \

@@ -8,6 +8,12 @@
                         per draw, the O3 (restated sampler_ref) token, and
                         the final position / history ring checksum.
   configs_o1.json       O1 tokens for small seeded instances of c1-c5.
+  fp16_data.json        the reference's own src/data.c fp16 helpers (compiled
+                        into oracle/_ref/): float_to_fp16 on 64 binary32 bit
+                        patterns, getDataFP16(15001, 4096, 102400) at 64
+                        (k, n) positions (the LM-head weights of the
+                        validation run, src/validation.c:6174), and
+                        transpose_block16(QUANT_FP16) of a 16 x 5 matrix.
 
 Run from the repository root:  python tests/golden/make_golden.py
 """
@@ -77,9 +83,48 @@ def configs_fixture():
     return out
 
 
+def fp16_fixture():
+    import ctypes
+    ref = O.ref_data_lib()
+    if ref is None:
+        raise SystemExit("oracle/_ref/libref_data.so missing: run `make -C oracle` with the reference present")
+    ref.float_to_fp16.restype = ctypes.c_uint16
+    ref.float_to_fp16.argtypes = [ctypes.c_float]
+    ref.getDataFP16.restype = ctypes.c_void_p
+    ref.getDataFP16.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    ref.transpose_block16.restype = None
+    ref.transpose_block16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    libc = ctypes.CDLL(None)
+    libc.free.argtypes = [ctypes.c_void_p]
+    rng = np.random.default_rng(5)
+    fixed = [0.0, -0.0, 1.0, -1.0, 65504.0, 65520.0, 70000.0, 1e-5, 6.1035156e-05, 5.9604645e-08, 2.9e-08,
+             1e-9, 0.1, -0.3333333, 3.14159265, np.inf, -np.inf, 1e30]
+    f = np.array(fixed + list(rng.normal(0, 4, 30)) + list(rng.uniform(-1, 1, 16)), np.float32)
+    fbits = f.view(np.uint32)
+    hbits = [int(ref.float_to_fp16(float(v))) for v in f]
+    K, V = 4096, 102400
+    ptr = ref.getDataFP16(15001, K, V)
+    data = np.ctypeslib.as_array(ctypes.cast(ptr, ctypes.POINTER(ctypes.c_uint16)), shape=(K * V,))
+    pos = [(0, 0), (0, 1), (1, 0), (K - 1, V - 1), (K - 1, 0), (0, V - 1)] + \
+        [(int(i), int(j)) for i, j in zip(rng.integers(0, K, 58), rng.integers(0, V, 58))]
+    gvals = [int(data[i * V + j]) for i, j in pos]
+    libc.free(ptr)
+    w = rng.integers(0, 65536, (16, 5), dtype=np.uint16)
+    out = np.zeros(16 * 5, np.uint16)
+    ref.transpose_block16(w.ctypes.data, out.ctypes.data, 16, 5, 16)
+    return {"float_to_fp16": {"in_bits": [int(b) for b in fbits], "out_bits": hbits},
+            "get_data_fp16": {"seed": 15001, "M": K, "N": V, "pos": pos, "bits": gvals},
+            "transpose_block16": {"K": 16, "V": 5, "in": w.reshape(-1).tolist(), "out": out.tolist()},
+            "source": "reference src/data.c float_to_fp16 / getDataFP16 / transpose_block16, "
+                      "compiled by oracle/Makefile"}
+
+
 def main():
+    only = sys.argv[1:]
     for name, fn in [("get_data_777001.json", get_data_fixture), ("validator_o1.json", validator_fixture),
-                     ("configs_o1.json", configs_fixture)]:
+                     ("configs_o1.json", configs_fixture), ("fp16_data.json", fp16_fixture)]:
+        if only and name not in only:
+            continue
         with open(os.path.join(HERE, name), "w") as f:
             json.dump(fn(), f, indent=1)
         print("wrote", name)

@@ -20,7 +20,7 @@ def declared_entry_points():
             continue
         src = open(os.path.join(ROOT, "include", fn)).read()
         src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-        for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b(pss_\w+|pgl_\w+)\s*\(", src, flags=re.M):
+        for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b(pss_\w+|pgl_\w+|plh_\w+)\s*\(", src, flags=re.M):
             names.add(m.group(1))
     return names
 
@@ -28,7 +28,7 @@ def declared_entry_points():
 def test_library_exports_every_declared_symbol():
     L = S.lib()
     names = declared_entry_points()
-    assert "pss_create" in names and "pss_enqueue" in names
+    assert "pss_create" in names and "pss_enqueue" in names and "plh_logits" in names
     missing = [n for n in sorted(names) if not hasattr(L, n)]
     assert not missing, f"declared but not exported: {missing}"
 
