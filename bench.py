@@ -368,6 +368,9 @@ def main():
     if args.lmhead_only:
         log("lm head (K 4096 x V 102400)")
         print(json.dumps({"lmhead": bench_lmhead(args.lmhead_steps)}), flush=True)
+        if args.copy_calib:
+            copy_calibration(256 * 102400 * 4)
+            log("copy calibration:", 256 * 102400 * 4, "bytes per copy")
         return
     if args.latency_only:
         log("latency (batch 1)")
