@@ -747,12 +747,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t pss_row_rsrc(const pss_args& a
     return __builtin_amdgcn_make_buffer_rsrc((void*)rowp, (short)0, (int)(a.V * esz), PSS_BUF_DW3);
 }
 
+/* Buffer-load cache policy of the fused form's logits stream: nontemporal.
+ * Every logit is read once per step; at the headline batch (6 x 105 MB
+ * rotating, beyond the last-level cache) this takes a step from 30.6 to
+ * 28.8 us.  The small-batch and split forms keep the default policy: a
+ * batch-1 decode chain over 64 rows (26 MB, within the L2 caches) is 1.9 us
+ * slower per step with the hint. */
+#define PSS_NT 2
+
 /* Item s of a row into the wave's staging area.  vec_ok (16-byte aligned
- * rows, V * element size a multiple of 16): raw buffer loads straight to LDS,
- * nothing waited for and no registers held; the hardware returns 0 for ids
- * at or beyond V.  Otherwise one buffer load per element into registers,
+ * rows, V * element size a multiple of 16): raw buffer loads straight to LDS
+ * (nontemporal), nothing waited for and no registers held; the hardware
+ * returns 0 for ids at or beyond V.  Otherwise one buffer load per element into registers,
  * waited for, then copied to the staging area. */
-template <int EPT, int DT>
+template <int EPT, int DT, int CPOL = 0>
 __device__ __forceinline__ void pss_wave_issue(const pss_args& a, uint32_t row, uint32_t s,
                                                pss_wave_lds<EPT, DT>& wl) {
     using Gm = pss_wgeom<EPT, DT>;
@@ -766,7 +774,7 @@ __device__ __forceinline__ void pss_wave_issue(const pss_args& a, uint32_t row, 
         for (int li = 0; li < NL; ++li)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rs, (__attribute__((address_space(3))) void*)&wl.stage[li][0], 16, (int)(lane * 16u),
-                (int)((base + (uint32_t)li * (PSS_WAVE * E)) * esz), 0, 0);
+                (int)((base + (uint32_t)li * (PSS_WAVE * E)) * esz), 0, CPOL);
     } else {
 #pragma unroll
         for (int li = 0; li < NL; ++li) {
@@ -945,7 +953,7 @@ __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, u
         /* loads first, parameters after: the item and window ids are in
          * flight while the row's parameters arrive (an uncovered row's
          * staged item is never read) */
-        pss_wave_issue<EPT, DT>(a, row, s, wl);
+        pss_wave_issue<EPT, DT, FUSED ? PSS_NT : 0>(a, row, s, wl);
         pss_wave_side_load_all(a, row, sd);
     }
     sample_params sp = params[row];
@@ -953,7 +961,7 @@ __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, u
     if (SMALL) {
         if (act) pss_wave_side_trim(a, sp, sd);
     } else if (cov) {
-        pss_wave_issue<EPT, DT>(a, row, s, wl);
+        pss_wave_issue<EPT, DT, FUSED ? PSS_NT : 0>(a, row, s, wl);
         pss_wave_side_load(a, row, sp, sd, !FUSED);
     }
     for (uint32_t r = 0; r < R; ++r) {
@@ -1051,7 +1059,7 @@ __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, u
             pss_wait_mem(); /* the staging area is free again */
             __asm__ __volatile__("" ::: "memory");
             if (ncov) {
-                pss_wave_issue<EPT, DT>(a, nrow, ns, wl);
+                pss_wave_issue<EPT, DT, FUSED ? PSS_NT : 0>(a, nrow, ns, wl);
                 pss_wave_side_load(a, nrow, nsp, nsd, !FUSED);
                 __asm__ __volatile__("" ::: "memory");
             }
@@ -1140,7 +1148,7 @@ __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, u
                 if (lane == 0u) joint[wave] = ((unsigned long long)row << 32) | T;
             }
         } else if (ncov) {
-            pss_wave_issue<EPT, DT>(a, nrow, ns, wl);
+            pss_wave_issue<EPT, DT, FUSED ? PSS_NT : 0>(a, nrow, ns, wl);
             pss_wave_side_load(a, nrow, nsp, nsd, !FUSED);
         }
         __syncthreads();
