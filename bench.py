@@ -13,7 +13,9 @@ A "step" is one pss_enqueue over a batch of logit rows resident in HBM.
   latency   batch 1 (config c2; the small-batch form, pss_small_kernel):
             launch-to-token p50/p90 (host clock, token stored by the kernel
             into pinned host memory), per-step GPU time, and steady
-            decode-group us/token through the C generate loop.
+            decode-group us/token through the C generate loops (per-group
+            readback, pinned tokens, and pipelined: the next group queued
+            before the current one is read).
   c3/c4/c5  the other batched configurations, rows/s and GB/s.
   lmhead    the LM head before the sampler (RMSNorm + fp16 GEMV over a
             4,096 x 102,400 block-transposed head): us per call and HBM GB/s
@@ -171,6 +173,11 @@ def bench_latency(steps):
     s.set_params(w.params, np.zeros(1, np.uint32))
     s.set_history(w.history)
     toks_pin, rp = G.generate(s, table, steps, rows=1, rng_mode=S.RNG_PHILOX, pinned=pinned)
+    # the pipelined loop: the next group is queued before the current one is
+    # read (gated passes), so the GPU runs the steps back to back
+    s.set_params(w.params, np.zeros(1, np.uint32))
+    s.set_history(w.history)
+    toks_pipe, rq = G.generate(s, table, steps, rows=1, rng_mode=S.RNG_PHILOX, pinned=pinned, pipelined=True)
     s.close()
     pinned.free()
     for d in dev:
@@ -179,7 +186,8 @@ def bench_latency(steps):
                 gpu_us_p50=pct(gpu_us, 50), gpu_us_p90=pct(gpu_us, 90), back_to_back_us_per_step=b2b_us,
                 decode_group_us_per_token=r["wall_us"] / max(r["emitted"], 1),
                 decode_group_pinned_us_per_token=rp["wall_us"] / max(rp["emitted"], 1),
-                decode_group_tokens_agree=bool(toks_gen == toks_pin))
+                decode_pipelined_us_per_token=rq["wall_us"] / max(rq["emitted"], 1),
+                decode_group_tokens_agree=bool(toks_gen == toks_pin == toks_pipe))
 
 
 def bench_lmhead(steps, K=4096, V=102400, rows_list=(1, 4)):

@@ -78,6 +78,25 @@ pss_status pgl_generate_pinned(pss_sampler* s, const pgl_config* cfg, pgl_logits
                                volatile uint32_t* pinned_host, pgl_result* out);
 
 /*
+ * The decode loop with the next group queued before the current one is read
+ * (no counterpart in the reference, which waits for each group before it
+ * submits the next, src/generate.c:1139-1149): the prefill-final pass and the
+ * first two decode groups are queued at once, and each time the host has read
+ * a group's tokens (pinned memory, as pgl_generate_pinned) it queues the group
+ * after the next, so the GPU never waits for the host.  The passes are
+ * PSS_ENQ_GATED with the group's sequence number and cfg->eos: a group queued
+ * after the one whose row 0 drew EOS does nothing, so tokens, result slots and
+ * the final state equal pgl_generate's.  A stop asked by `emit` (not EOS, not
+ * max_new) comes after up to two groups have been queued beyond it: those
+ * groups run and advance the state.  pinned_dev / pinned_host: at least
+ * 9 * rows u32 (prefill slot, two group regions).  out->groups counts the
+ * groups whose tokens were read.
+ */
+pss_status pgl_generate_pipelined(pss_sampler* s, const pgl_config* cfg, pgl_logits_fn logits, void* lctx,
+                                  pgl_emit_fn emit, void* ectx, uint32_t* pinned_dev,
+                                  volatile uint32_t* pinned_host, pgl_result* out);
+
+/*
  * Scoring consumption of generateScore (src/generate.c:1198-1228) for row 0:
  * ids[0..n) are scored in groups of PGL_DECODE_GROUP passes; per group the
  * targets go to the pass slots (pss_set_score_targets, the reference's

@@ -104,6 +104,9 @@ typedef struct {
     void* split_event;        /* hipEvent_t recorded on the sampler's stream after
                                  the first kernel of the step (with PSS_ENQ_SPLIT:
                                  per-kernel timing); NULL: none                  */
+    uint32_t gate_seq;        /* with PSS_ENQ_GATED: sequence number of the pass's
+                                 decode group (> 0, increasing group by group)   */
+    uint32_t eos;             /* with PSS_ENQ_GATED: the id that closes the gate */
 } pss_enqueue_opts;
 
 /* Run the one-workgroup-per-row general kernel instead of the streaming kernel
@@ -118,6 +121,15 @@ typedef struct {
 #define PSS_ENQ_SPLIT 2u
 #define PSS_ENQ_FUSED 4u
 #define PSS_ENQ_SMALL 8u
+/* Gated pass (no counterpart in the reference, whose host waits for each
+ * decode group before it submits the next): the sampler keeps one device word
+ * eos_at (reset by pss_reset_gate).  A gated pass does nothing at all (no
+ * output, no state change) if eos_at < opts.gate_seq; when row 0 draws
+ * opts.eos it lowers eos_at to opts.gate_seq.  Passes of one decode group
+ * share gate_seq, so the rest of the group that drew EOS still runs and every
+ * later group is skipped: a caller can queue group n + 1 before it has read
+ * group n's tokens and still end in the state of the unpipelined loop. */
+#define PSS_ENQ_GATED 16u
 
 /* Words per row of kept_mask. */
 uint32_t pss_mask_words(uint32_t vocab);
@@ -191,6 +203,9 @@ pss_status pss_enqueue_ex(pss_sampler* s, const void* logits, uint32_t dtype, ui
 /* Synchronize the sampler's stream and copy result slots [rows][4] and/or the
  * last token of each row [rows] to host memory (either may be NULL). */
 pss_status pss_read_results(pss_sampler* s, uint32_t rows, uint32_t* results, uint32_t* tokens);
+
+/* Re-open the gate of PSS_ENQ_GATED passes (eos_at = 0xFFFFFFFF), stream-ordered. */
+pss_status pss_reset_gate(pss_sampler* s);
 
 /* Synchronize and copy per-row state to host (any pointer may be NULL):
  * history [rows][1024], position [rows], rng [rows], philox step [rows]. */

@@ -54,6 +54,9 @@ struct pss_args {
     uint32_t vec_ok;      /* rows 16-byte aligned, V * element size a multiple of 16 */
     uint32_t kmax_cov;    /* largest top-k the launched streaming form covers */
     uint32_t wmax_cov;    /* largest window it covers */
+    uint32_t* gate;       /* gated passes: the sampler's eos_at word, else NULL */
+    uint32_t gate_seq;
+    uint32_t eos;
 };
 
 /* Global-memory pointers.  Pointers that reach a kernel inside a struct are
@@ -81,6 +84,14 @@ __device__ __forceinline__ void pss_globalize(pss_args& a) {
     a.probs = pss_glob(a.probs);
     a.host_tokens = pss_glob(a.host_tokens);
     a.ws = pss_glob((char*)a.ws);
+    a.gate = pss_glob(a.gate);
+}
+
+/* A gated pass whose decode group follows the one that drew EOS does
+ * nothing.  Every workgroup of a launch reads the same answer: the only store
+ * to eos_at during a launch lowers it to that launch's own gate_seq. */
+__device__ __forceinline__ bool pss_gate_closed(const pss_args& a) {
+    return a.gate && __hip_atomic_load(a.gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < a.gate_seq;
 }
 
 /* Wait until every memory operation this wave issued has completed. */

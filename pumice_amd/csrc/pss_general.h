@@ -49,6 +49,8 @@ __device__ __forceinline__ void pss_epilogue_pre(const pss_args& a, uint32_t row
             pss_out(&a.rng[row], new_rng);
     }
     if (a.do_inc) pss_out(&a.position[row], pos + 1u);
+    if (a.gate && row == 0u && tok == a.eos)
+        (void)__hip_atomic_fetch_min(a.gate, a.gate_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (a.host_tokens) a.host_tokens[row] = tok;
     if (a.info) a.info[row] = inf;
 }
@@ -404,6 +406,7 @@ __global__ void __launch_bounds__(PSS_GEN_NT) pss_general_kernel(pss_args a) {
     __shared__ pss_gen_shared sh;
     __shared__ uint32_t bits[PSS_MAX_VOCAB / 32];
     pss_globalize(a);
+    if (pss_gate_closed(a)) return;
     pss_general_row<PSS_GEN_NT>(a, blockIdx.x, sh, bits, PSS_MAX_VOCAB / 32);
 }
 

@@ -114,7 +114,7 @@ pss_status pgl_generate_pinned(pss_sampler* s, const pgl_config* cfg, pgl_logits
     double t0 = now_us();
     uint32_t pos = cfg->start_pos;
     pss_status st;
-    pss_enqueue_opts o = {NULL, NULL, NULL, 0, NULL, 0, NULL};
+    pss_enqueue_opts o = {NULL, NULL, NULL, 0, NULL, 0, NULL, 0, 0};
 
     /* prefill-final pass: slot 0, no position increment (generate.c:642) */
     uint32_t posv[256];
@@ -209,7 +209,7 @@ pss_status pgl_step_latency(pss_sampler* s, pgl_logits_fn logits, void* lctx, ui
                             uint32_t* pinned_dev, volatile uint32_t* pinned_host, double* lat_us,
                             uint32_t* tokens) {
     if (!s || !logits || !pinned_dev || !pinned_host || !lat_us) return PSS_ERR_INVALID_ARG;
-    pss_enqueue_opts o = {NULL, NULL, NULL, 0, pinned_dev, 0, NULL};
+    pss_enqueue_opts o = {NULL, NULL, NULL, 0, pinned_dev, 0, NULL, 0, 0};
     for (uint32_t i = 0; i < steps; ++i) {
         const void* x = logits(lctx, i);
         pinned_host[0] = 0xFFFFFFFFu;
@@ -226,4 +226,117 @@ pss_status pgl_step_latency(pss_sampler* s, pgl_logits_fn logits, void* lctx, ui
     }
     /* The kernel's remaining state writes are stream-ordered; wait for them. */
     return pss_read_results(s, 1, NULL, NULL);
+}
+
+/* One decode group of the pipelined loop: `cur` gated passes with sequence
+ * number `seq`, tokens into the pinned region `reg` (pass p at p * rows). */
+static pss_status pipelined_group(pss_sampler* s, const pgl_config* cfg, pgl_logits_fn logits, void* lctx,
+                                  uint32_t pos0, uint32_t cur, uint32_t seq, uint32_t* reg_dev,
+                                  volatile uint32_t* reg_host) {
+    const uint32_t rows = cfg->rows;
+    for (uint32_t p = 0; p < cur; ++p) reg_host[p * rows] = 0xFFFFFFFFu;
+    __atomic_thread_fence(__ATOMIC_SEQ_CST);
+    pss_enqueue_opts o;
+    memset(&o, 0, sizeof o);
+    o.flags = PSS_ENQ_GATED;
+    o.gate_seq = seq;
+    o.eos = cfg->eos;
+    for (uint32_t p = 0; p < cur; ++p) {
+        o.host_tokens = reg_dev + p * rows;
+        const pss_status st = pss_enqueue_ex(s, logits(lctx, pos0 + p), cfg->dtype, cfg->row_stride, rows,
+                                             cfg->mode, 1, p, cfg->rng_mode, &o);
+        if (st != PSS_OK) return st;
+    }
+    return PSS_OK;
+}
+
+pss_status pgl_generate_pipelined(pss_sampler* s, const pgl_config* cfg, pgl_logits_fn logits, void* lctx,
+                                  pgl_emit_fn emit, void* ectx, uint32_t* pinned_dev,
+                                  volatile uint32_t* pinned_host, pgl_result* out) {
+    if (!s || !cfg || !logits || !emit || !out || !pinned_dev || !pinned_host || cfg->max_new == 0 ||
+        cfg->rows == 0 || cfg->rows > 256)
+        return PSS_ERR_INVALID_ARG;
+    const uint32_t rows = cfg->rows;
+    pgl_result r = {0, 1, 0, 0.0};
+    double t0 = now_us();
+    pss_status st = pss_reset_gate(s);
+    if (st != PSS_OK) return st;
+    uint32_t posv[256];
+    for (uint32_t i = 0; i < rows; ++i) posv[i] = cfg->start_pos;
+    st = pss_set_position(s, 0, rows, posv);
+    if (st != PSS_OK) return st;
+
+    /* prefill-final pass: slot 0, no increment, sequence number 1 */
+    pinned_host[0] = 0xFFFFFFFFu;
+    __atomic_thread_fence(__ATOMIC_SEQ_CST);
+    pss_enqueue_opts o;
+    memset(&o, 0, sizeof o);
+    o.flags = PSS_ENQ_GATED;
+    o.gate_seq = 1u;
+    o.eos = cfg->eos;
+    o.host_tokens = pinned_dev;
+    st = pss_enqueue_ex(s, logits(lctx, cfg->start_pos), cfg->dtype, cfg->row_stride, rows, cfg->mode, 0, 0,
+                        cfg->rng_mode, &o);
+    if (st != PSS_OK) return st;
+
+    const uint32_t decode = cfg->max_new - 1u;
+    const uint32_t ngroups = (decode + PGL_DECODE_GROUP - 1u) / PGL_DECODE_GROUP;
+    uint32_t queued = 0;
+    /* group g: passes at positions start + 4g + p, region g % 2, sequence 2 + g */
+#define PGL_GROUP_CUR(g) (decode - (g) * PGL_DECODE_GROUP < PGL_DECODE_GROUP ? decode - (g) * PGL_DECODE_GROUP \
+                                                                              : PGL_DECODE_GROUP)
+#define PGL_REGION(g) (rows + ((g) & 1u) * PGL_DECODE_GROUP * rows)
+    while (queued < ngroups && queued < 2u) {
+        st = pipelined_group(s, cfg, logits, lctx, cfg->start_pos + queued * PGL_DECODE_GROUP, PGL_GROUP_CUR(queued),
+                             2u + queued, pinned_dev + PGL_REGION(queued), pinned_host + PGL_REGION(queued));
+        if (st != PSS_OK) return st;
+        queued++;
+    }
+
+    st = wait_token(s, rows, &pinned_host[0]);
+    if (st != PSS_OK) return st;
+    uint32_t tok = pinned_host[0];
+    r.emitted = 1;
+    int stop = emit(ectx, tok);
+    if (tok == cfg->eos || stop) {
+        r.finish_reason = 0;
+        r.wall_us = now_us() - t0;
+        *out = r;
+        return pss_read_results(s, rows, NULL, NULL);
+    }
+    for (uint32_t g = 0; g < ngroups; ++g) {
+        const uint32_t cur = PGL_GROUP_CUR(g);
+        volatile uint32_t* reg = pinned_host + PGL_REGION(g);
+        st = wait_token(s, rows, &reg[(cur - 1u) * rows]);
+        if (st != PSS_OK) return st;
+        uint32_t toks[PGL_DECODE_GROUP];
+        int eos_seen = 0;
+        for (uint32_t j = 0; j < cur; ++j) {
+            toks[j] = reg[j * rows]; /* row 0, pass j */
+            if (toks[j] == cfg->eos) eos_seen = 1;
+        }
+        r.groups++;
+        if (!eos_seen && queued < ngroups) { /* region g % 2 is free again */
+            st = pipelined_group(s, cfg, logits, lctx, cfg->start_pos + queued * PGL_DECODE_GROUP,
+                                 PGL_GROUP_CUR(queued), 2u + queued, pinned_dev + PGL_REGION(queued),
+                                 pinned_host + PGL_REGION(queued));
+            if (st != PSS_OK) return st;
+            queued++;
+        }
+        for (uint32_t j = 0; j < cur; ++j) {
+            r.emitted++;
+            stop = emit(ectx, toks[j]);
+            if (toks[j] == cfg->eos || stop) {
+                r.finish_reason = 0;
+                r.wall_us = now_us() - t0;
+                *out = r;
+                return pss_read_results(s, rows, NULL, NULL);
+            }
+        }
+    }
+#undef PGL_GROUP_CUR
+#undef PGL_REGION
+    r.wall_us = now_us() - t0;
+    *out = r;
+    return pss_read_results(s, rows, NULL, NULL);
 }

@@ -61,6 +61,7 @@ static void free_all(pss_sampler* s) {
     (void)hipFree(s->d_result);
     (void)hipFree(s->d_tokens);
     (void)hipFree(s->d_targets);
+    (void)hipFree(s->d_gate);
     (void)hipFree(s->d_ws);
     free(s->h_topk);
     free(s->h_wlen);
@@ -111,6 +112,7 @@ extern "C" pss_status pss_create(pss_sampler** out, uint32_t vocab, uint32_t max
         hipMalloc((void**)&s->d_result, 4 * R * PSS_RESULT_SLOTS) != hipSuccess ||
         hipMalloc((void**)&s->d_tokens, 4 * R) != hipSuccess ||
         hipMalloc((void**)&s->d_targets, 4 * R * PSS_RESULT_SLOTS) != hipSuccess ||
+        hipMalloc((void**)&s->d_gate, 256) != hipSuccess ||
         (s->ws_bytes && hipMalloc(&s->d_ws, s->ws_bytes) != hipSuccess)) {
         free_all(s);
         return PSS_ERR_ALLOC;
@@ -124,6 +126,7 @@ extern "C" pss_status pss_create(pss_sampler** out, uint32_t vocab, uint32_t max
     if (st == PSS_OK) st = fill_u32(s->stream, s->d_result, R * PSS_RESULT_SLOTS, 0u);
     if (st == PSS_OK) st = fill_u32(s->stream, s->d_tokens, R, 0u);
     if (st == PSS_OK) st = fill_u32(s->stream, s->d_targets, R * PSS_RESULT_SLOTS, 0u);
+    if (st == PSS_OK) st = fill_u32(s->stream, s->d_gate, 64, 0xFFFFFFFFu);
     if (st == PSS_OK && s->ws_bytes) st = fill_u32(s->stream, (uint32_t*)s->d_ws, s->ws_bytes / 4, 0u);
     if (st == PSS_OK && hipStreamSynchronize(s->stream) != hipSuccess) st = PSS_ERR_HIP;
     if (st != PSS_OK) {
@@ -252,8 +255,18 @@ static pss_args make_args(pss_sampler* s, const void* logits, uint32_t dtype, ui
         a.probs = o->probs;
         a.probs_stride = o->probs_stride;
         a.host_tokens = o->host_tokens;
+        if (o->flags & PSS_ENQ_GATED) {
+            a.gate = s->d_gate;
+            a.gate_seq = o->gate_seq;
+            a.eos = o->eos;
+        }
     }
     return a;
+}
+
+extern "C" pss_status pss_reset_gate(pss_sampler* s) {
+    if (!s) return PSS_ERR_INVALID_ARG;
+    return fill_u32(s->stream, s->d_gate, 1, 0xFFFFFFFFu);
 }
 
 extern "C" pss_status pss_enqueue_ex(pss_sampler* s, const void* logits, uint32_t dtype,
@@ -265,6 +278,8 @@ extern "C" pss_status pss_enqueue_ex(pss_sampler* s, const void* logits, uint32_
     if (mode != PSS_MODE_GREEDY && mode != PSS_MODE_SAMPLE && mode != PSS_MODE_SCORE) return PSS_ERR_INVALID_ARG;
     if (rng_mode != PSS_RNG_XORSHIFT32 && rng_mode != PSS_RNG_PHILOX) return PSS_ERR_INVALID_ARG;
     if (pass_idx >= PSS_RESULT_SLOTS || row_stride < s->V) return PSS_ERR_INVALID_ARG;
+    if (opts && (opts->flags & PSS_ENQ_GATED) && (mode == PSS_MODE_SCORE || opts->gate_seq == 0))
+        return PSS_ERR_INVALID_ARG;
     if (opts && opts->probs && opts->probs_stride < s->V) return PSS_ERR_INVALID_ARG;
     pss_args a = make_args(s, logits, dtype, row_stride, mode, do_increment, pass_idx, rng_mode, opts);
     if (mode == PSS_MODE_SCORE) {

@@ -25,6 +25,7 @@ struct pss_sampler {
     uint32_t* d_result;
     uint32_t* d_tokens;
     uint32_t* d_targets; /* scoring targets [max_rows][PSS_RESULT_SLOTS] */
+    uint32_t* d_gate;    /* eos_at of PSS_ENQ_GATED passes (one word, 256-byte allocation) */
     void* d_ws;       /* streaming-kernel workspace: per-row bounds and candidate pools */
     size_t ws_bytes;
     uint32_t* h_topk; /* host copy of each row's topK (picks the kernel variant) */

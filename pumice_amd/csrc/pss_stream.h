@@ -1265,6 +1265,7 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_seg_kernel(pss_args a, uint32_
     __shared__ pss_wave_lds<EPT, DT> lds[PSS_SEG_NW];
     __shared__ unsigned long long joint[PSS_SEG_NW]; /* (row << 32) | per-wave certificate */
     pss_globalize(a);
+    if (pss_gate_closed(a)) return;
     const uint32_t i0 = blockIdx.x * per_wg;
     const uint32_t i1 = i0 + per_wg < n_items ? i0 + per_wg : n_items;
     if (i0 >= i1) return;
@@ -1309,6 +1310,7 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_row_kernel(pss_args a, uint32_
     __shared__ RL rl;
     __shared__ uint32_t win[WIDE ? PSS_MAX_PENALTY_LEN : 1];
     pss_globalize(a);
+    if (pss_gate_closed(a)) return;
     const uint32_t row = blockIdx.x, tid = pss_tid();
     const sample_params sp = params[row];
     pss_row_pre pre;
@@ -1509,6 +1511,7 @@ __global__ void __launch_bounds__(PSS_ST_NT) pss_fin_kernel(pss_args a, uint32_t
     __shared__ pss_fin_shared sh;
     __shared__ uint32_t bits[PSS_MAX_VOCAB / 32];
     pss_globalize(a);
+    if (pss_gate_closed(a)) return;
     sample_params sp;
     pss_row_pre pre;
     pss_load_row_state(a, params, blockIdx.x, sp, pre);
@@ -1542,6 +1545,7 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_small_kernel(pss_args a, uint3
     __shared__ unsigned long long joint[PSS_SEG_NW];
     __shared__ uint32_t last;
     pss_globalize(a);
+    if (pss_gate_closed(a)) return;
     const uint32_t row = blockIdx.x / GW, g = blockIdx.x - row * GW;
     const uint32_t s0 = g * NS / GW, s1 = (g + 1u) * NS / GW;
     const uint32_t tid = pss_tid();

@@ -38,6 +38,8 @@ def _lib():
         L.pgl_generate.restype = ctypes.c_int
         L.pgl_generate_pinned.argtypes = [P, P, P, P, P, P, P, P, P]
         L.pgl_generate_pinned.restype = ctypes.c_int
+        L.pgl_generate_pipelined.argtypes = [P, P, P, P, P, P, P, P, P]
+        L.pgl_generate_pipelined.restype = ctypes.c_int
         L.pgl_score.argtypes = [P, P, P, u32, u64, P, u32, u32, P, P]
         L.pgl_score.restype = ctypes.c_int
         L.pgl_step_latency.argtypes = [P, P, P, u32, u64, u32, u32, P, P, P, P]
@@ -62,10 +64,11 @@ class LogitsTable:
 
 
 def generate(sampler, table, max_new, rows=1, dtype=S.DTYPE_F32, row_stride=None, mode=S.MODE_SAMPLE,
-             rng_mode=S.RNG_XORSHIFT32, eos=0xFFFFFFFF, start_pos=0, stop_after=None, pinned=None):
-    """pgl_generate (or, with `pinned` a hip.PinnedBuffer of at least
-    rows * 4 u32, pgl_generate_pinned); returns (emitted tokens of row 0,
-    result dict)."""
+             rng_mode=S.RNG_XORSHIFT32, eos=0xFFFFFFFF, start_pos=0, stop_after=None, pinned=None,
+             pipelined=False):
+    """pgl_generate; with `pinned` (a hip.PinnedBuffer of at least rows * 4
+    u32) pgl_generate_pinned; with `pipelined` too (at least rows * 9 u32)
+    pgl_generate_pipelined.  Returns (emitted tokens of row 0, result dict)."""
     out = []
 
     def _emit(ctx, tok):
@@ -76,16 +79,21 @@ def generate(sampler, table, max_new, rows=1, dtype=S.DTYPE_F32, row_stride=None
     cfg = CConfig(max_new, eos, rows, dtype, row_stride or sampler.vocab, mode, rng_mode, start_pos)
     res = CResult()
     if pinned is None:
+        if pipelined:
+            raise ValueError("the pipelined loop needs a pinned buffer")
+        name = "pgl_generate"
         st = _lib().pgl_generate(sampler.handle, ctypes.byref(cfg), table.fn, table.ctx,
                                  ctypes.cast(emit, ctypes.c_void_p), None, ctypes.byref(res))
     else:
-        if pinned.nbytes < 4 * rows * 4:
-            raise ValueError("pinned buffer smaller than rows * 4 u32")
-        st = _lib().pgl_generate_pinned(sampler.handle, ctypes.byref(cfg), table.fn, table.ctx,
-                                        ctypes.cast(emit, ctypes.c_void_p), None, pinned.dev_ptr, pinned.ptr,
-                                        ctypes.byref(res))
+        need = (9 if pipelined else 4) * rows * 4
+        if pinned.nbytes < need:
+            raise ValueError(f"pinned buffer smaller than {need} bytes")
+        name = "pgl_generate_pipelined" if pipelined else "pgl_generate_pinned"
+        st = getattr(_lib(), name)(sampler.handle, ctypes.byref(cfg), table.fn, table.ctx,
+                                   ctypes.cast(emit, ctypes.c_void_p), None, pinned.dev_ptr, pinned.ptr,
+                                   ctypes.byref(res))
     if st != 0:
-        raise S.PssError(st, "pgl_generate" if pinned is None else "pgl_generate_pinned")
+        raise S.PssError(st, name)
     return out, dict(emitted=res.emitted, finish_reason=res.finish_reason, groups=res.groups,
                      wall_us=res.wall_us)
 

@@ -31,6 +31,7 @@ ENQ_GENERAL = 1
 ENQ_SPLIT = 2
 ENQ_FUSED = 4
 ENQ_SMALL = 8
+ENQ_GATED = 16
 
 STATUS = {0: "ok", 1: "invalid argument", 2: "allocation failed", 3: "HIP runtime error",
           4: "unsupported", 5: "no gfx950 device"}
@@ -57,7 +58,7 @@ class CEnqueueOpts(ctypes.Structure):
     _fields_ = [("row_info", ctypes.c_void_p), ("kept_mask", ctypes.c_void_p),
                 ("probs", ctypes.c_void_p), ("probs_stride", ctypes.c_uint64),
                 ("host_tokens", ctypes.c_void_p), ("flags", ctypes.c_uint32),
-                ("split_event", ctypes.c_void_p)]
+                ("split_event", ctypes.c_void_p), ("gate_seq", ctypes.c_uint32), ("eos", ctypes.c_uint32)]
 
 
 class CStatePtrs(ctypes.Structure):
@@ -68,7 +69,7 @@ EXPORTS = [
     "pss_create", "pss_destroy", "pss_set_params", "pss_reset_history", "pss_set_history",
     "pss_set_position", "pss_enqueue", "pss_enqueue_ex", "pss_read_results", "pss_read_state",
     "pss_get_state_ptrs", "pss_sanitize_request", "pss_stream", "pss_status_string",
-    "pss_mask_words", "pss_set_score_targets",
+    "pss_mask_words", "pss_set_score_targets", "pss_reset_gate",
 ]
 
 
@@ -95,6 +96,7 @@ def lib():
         L.pss_set_history.argtypes = [P, u32, u32, P, u32]
         L.pss_set_position.argtypes = [P, u32, u32, P]
         L.pss_set_score_targets.argtypes = [P, u32, u32, u32, P]
+        L.pss_reset_gate.argtypes = [P]
         L.pss_enqueue.argtypes = [P, P, u32, u64, u32, u32, u32, u32, u32]
         L.pss_enqueue_ex.argtypes = [P, P, u32, u64, u32, u32, u32, u32, u32, P]
         L.pss_read_results.argtypes = [P, u32, P, P]
@@ -183,6 +185,9 @@ class Sampler:
         _ok(lib().pss_set_params(self.handle, row0, p.size, p.ctypes.data,
                                  None if s is None else s.ctypes.data), "pss_set_params")
 
+    def reset_gate(self):
+        _ok(lib().pss_reset_gate(self.handle), "pss_reset_gate")
+
     def reset_history(self, fill=SENTINEL, row0=0, rows=None):
         rows = self.max_rows - row0 if rows is None else rows
         _ok(lib().pss_reset_history(self.handle, row0, rows, fill), "pss_reset_history")
@@ -208,15 +213,18 @@ class Sampler:
 
     def enqueue(self, logits_ptr, dtype, row_stride, rows, mode=MODE_SAMPLE, do_increment=1,
                 pass_idx=0, rng_mode=RNG_XORSHIFT32, row_info=None, kept_mask=None, probs=None,
-                probs_stride=0, host_tokens=None, flags=0, split_event=None):
+                probs_stride=0, host_tokens=None, flags=0, split_event=None, gate_seq=0, eos=0xFFFFFFFF):
         """One step; logits_ptr and the optional outputs are device pointers (ints).
-        split_event: a hipEvent_t recorded between the step's two kernels."""
+        split_event: a hipEvent_t recorded between the step's two kernels.
+        gate_seq / eos: the decode-group sequence number and EOS id of an
+        ENQ_GATED pass."""
         if (row_info is None and kept_mask is None and probs is None and host_tokens is None
                 and not flags and split_event is None):
             st = lib().pss_enqueue(self.handle, logits_ptr, dtype, row_stride, rows, mode,
                                    do_increment, pass_idx, rng_mode)
         else:
-            o = CEnqueueOpts(row_info, kept_mask, probs, probs_stride, host_tokens, flags, split_event)
+            o = CEnqueueOpts(row_info, kept_mask, probs, probs_stride, host_tokens, flags, split_event,
+                             gate_seq, eos)
             st = lib().pss_enqueue_ex(self.handle, logits_ptr, dtype, row_stride, rows, mode,
                                       do_increment, pass_idx, rng_mode, ctypes.byref(o))
         _ok(st, "pss_enqueue")
