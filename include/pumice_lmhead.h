@@ -82,6 +82,30 @@ pss_status plh_transpose_block16(const uint16_t* w_kv, uint16_t* w_bt, uint32_t 
 
 void* plh_stream(plh_head* h);
 
+/* Source row formats of plh_pack_head. */
+#define PLH_SRC_BF16 0u
+#define PLH_SRC_FP16 1u
+
+/* Host: read a pruned-vocabulary map, pruned-vocab/mapping.npy (int32[V],
+ * pruned id -> original id), into out[expected]: NumPy format version 1,
+ * dtype '<i4', one dimension of length `expected`, as src/prune.c:32-57
+ * loadMapping requires.  PSS_ERR_INVALID_ARG on any mismatch (the reference
+ * exits). */
+pss_status plh_load_vocab_map(const char* path, uint32_t expected, int32_t* out);
+
+/* Device: build the block-transposed fp16 head from the model's lm_head rows
+ * src[src_rows][K] (bf16 or fp16, row-major, device memory) as the reference
+ * builds it at load time: row n of the head is source row mapping[n]
+ * (mapping: host int32[V], every entry in [0, src_rows); NULL: n, the
+ * unpruned vocabulary, src_rows = V).  Values pass through the reference's
+ * conversions: the pruning gather re-encodes fp16 rows as bf16
+ * (src/prune.c:128-146, float_to_bf16), the loader converts bf16 (or fp16)
+ * to fp16 with the truncating float_to_fp16 (src/weights.c:520-566) and
+ * block-transposes (src/data.c:305-331).  Synchronous; allocates a temporary
+ * copy of the map.  w_bt: K * V halves. */
+pss_status plh_pack_head(const void* src, uint32_t src_dtype, uint32_t src_rows, uint32_t K,
+                         const int32_t* mapping, uint32_t V, uint16_t* w_bt, void* hip_stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -114,6 +114,10 @@ def lib():
         L.oracle_get_data_fp16.argtypes = [i32, i32, i32, P]
         L.oracle_transpose_block16_fp16.restype = None
         L.oracle_transpose_block16_fp16.argtypes = [P, P, u32, u32]
+        L.oracle_float_to_bf16_many.restype = None
+        L.oracle_float_to_bf16_many.argtypes = [P, P, u64]
+        L.oracle_pack_head.restype = None
+        L.oracle_pack_head.argtypes = [P, u32, u32, P, u32, P]
         L.oracle_lmhead_norm.restype = f32
         L.oracle_lmhead_norm.argtypes = [P, P, u32, P]
         L.oracle_lmhead_logits.restype = None
@@ -285,6 +289,30 @@ def transpose_block16(w_kv):
     K, V = w.shape
     out = np.zeros((K // 8, V, 8), np.uint16)
     lib().oracle_transpose_block16_fp16(_ptr(w), _ptr(out), K, V)
+    return out
+
+
+def float_to_bf16(f):
+    """src/data.c:194-200 over an array; returns uint16 bits."""
+    f = np.ascontiguousarray(f, np.float32)
+    b = np.zeros(f.shape, np.uint16)
+    lib().oracle_float_to_bf16_many(_ptr(f), _ptr(b), f.size)
+    return b
+
+
+def pack_head(src, src_dtype, mapping=None):
+    """The reference's load-time fp16 head (gather, conversions, transpose)
+    from lm_head rows src[src_rows][K] (uint16 bits; src_dtype 0 bf16, 1 fp16)
+    -> [K/8][V][8]."""
+    src = np.ascontiguousarray(src, np.uint16)
+    K = src.shape[1]
+    if mapping is None:
+        V, mp = src.shape[0], None
+    else:
+        m = np.ascontiguousarray(mapping, np.int32)
+        V, mp = m.size, _ptr(m)
+    out = np.zeros((K // 8, V, 8), np.uint16)
+    lib().oracle_pack_head(_ptr(src), src_dtype, K, mp, V, _ptr(out))
     return out
 
 

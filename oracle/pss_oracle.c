@@ -794,6 +794,54 @@ void oracle_transpose_block16_fp16(const uint16_t* w_kv, uint16_t* w_bt, uint32_
                 w_bt[((size_t)kb * V + n) * 8u + j] = w_kv[(size_t)(8u * kb + j) * V + n];
 }
 
+/* src/data.c:187-192: the bf16 bits are the high half of the binary32. */
+float oracle_bf16_to_float(uint16_t b) {
+    const uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* src/data.c:194-200: round to nearest, ties to even, by adding 0x7FFF plus
+ * the lowest kept bit before dropping the low half (no NaN special case). */
+uint16_t oracle_float_to_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+void oracle_float_to_bf16_many(const float* f, uint16_t* b, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) b[i] = oracle_float_to_bf16(f[i]);
+}
+
+/* Pruned (map given): gatherRows copies row map[v] (bf16 as is, fp16 through
+ * float_to_bf16(fp16_to_float)) into a bf16 tensor, which loadEmbedLike turns
+ * into float_to_fp16(bf16_to_float(.)).  Unpruned: loadEmbedLike reads the
+ * shard tensor directly (bf16 as above, fp16 through float_to_fp16 of its
+ * float value).  Both then transpose_block16 the [K][V] fp16 matrix. */
+void oracle_pack_head(const uint16_t* src, uint32_t src_dtype, uint32_t K, const int32_t* map, uint32_t V,
+                      uint16_t* w_bt) {
+    uint16_t* eng = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)K * V);
+    for (uint32_t v = 0; v < V; ++v) {
+        const uint16_t* row = src + (size_t)(map ? (uint32_t)map[v] : v) * K;
+        for (uint32_t k = 0; k < K; ++k) {
+            uint16_t raw = row[k];
+            float x;
+            if (src_dtype == 0u) {
+                x = oracle_bf16_to_float(raw);
+            } else if (map) {
+                x = oracle_bf16_to_float(oracle_float_to_bf16(oracle_fp16_to_float(raw)));
+            } else {
+                x = oracle_fp16_to_float(raw);
+            }
+            eng[(size_t)k * V + v] = oracle_float_to_fp16(x);
+        }
+    }
+    oracle_transpose_block16_fp16(eng, w_bt, K, V);
+    free(eng);
+}
+
 /* RMSNorm of LMHead-GEMV-Q16.comp:34-58 (src/validation.c:157-163 on the
  * CPU): rms = sqrt(sum x^2 / K + 1e-6), a = x gamma / rms.  The sum of squares
  * in the GPU's order: 256 strided binary64 partials (thread t: k = t, t + 256,

@@ -77,6 +77,16 @@ void oracle_fp16_to_float_many(const uint16_t* h, float* f, uint64_t n);
  * K-slice order (nslices slices, fmaf chains, partials added in slice order);
  * and the same GEMV in binary64 with sum |a w| for error bounds. */
 void oracle_transpose_block16_fp16(const uint16_t* w_kv, uint16_t* w_bt, uint32_t K, uint32_t V);
+/* src/data.c:187-200 bf16 conversions. */
+float oracle_bf16_to_float(uint16_t b);
+uint16_t oracle_float_to_bf16(float f);
+void oracle_float_to_bf16_many(const float* f, uint16_t* b, uint64_t n);
+/* The reference's load-time build of the fp16 head from lm_head rows
+ * src[src_rows][K] (src_dtype 0 bf16 / 1 fp16): src/prune.c:128-146 gather
+ * (fp16 rows re-encoded as bf16) when map is not NULL, src/weights.c:520-566
+ * conversion to fp16 and transpose into [K][V], src/data.c:305-331. */
+void oracle_pack_head(const uint16_t* src, uint32_t src_dtype, uint32_t K, const int32_t* map, uint32_t V,
+                      uint16_t* w_bt);
 float oracle_lmhead_norm(const float* x, const float* gamma, uint32_t K, float* a);
 void oracle_lmhead_logits(const float* a, const uint16_t* w_bt, uint32_t K, uint32_t V, uint32_t nslices,
                           float* out);

@@ -20,7 +20,7 @@ INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "libpumice_sampler.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-HIP_SOURCES = ["pss_sampler.hip", "plh_lmhead.hip"]
+HIP_SOURCES = ["pss_sampler.hip", "plh_lmhead.hip", "plh_pack.hip"]
 C_SOURCES = ["pss_generate.c"]
 HIP_FLAGS = [
     "--offload-arch=gfx950",

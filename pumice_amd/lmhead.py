@@ -13,7 +13,10 @@ TILE = 64
 SLICES = 4
 MAX_K = 65536
 
-EXPORTS = ["plh_create", "plh_destroy", "plh_logits", "plh_greedy", "plh_transpose_block16", "plh_stream"]
+SRC_BF16, SRC_FP16 = 0, 1
+
+EXPORTS = ["plh_create", "plh_destroy", "plh_logits", "plh_greedy", "plh_transpose_block16", "plh_stream",
+           "plh_load_vocab_map", "plh_pack_head"]
 
 _bound = False
 
@@ -30,7 +33,10 @@ def lib():
         L.plh_transpose_block16.argtypes = [P, P, u32, u32]
         L.plh_stream.argtypes = [P]
         L.plh_stream.restype = P
-        for n in ("plh_create", "plh_destroy", "plh_logits", "plh_greedy", "plh_transpose_block16"):
+        L.plh_load_vocab_map.argtypes = [ctypes.c_char_p, u32, P]
+        L.plh_pack_head.argtypes = [P, u32, u32, u32, P, u32, P, P]
+        for n in ("plh_create", "plh_destroy", "plh_logits", "plh_greedy", "plh_transpose_block16",
+                  "plh_load_vocab_map", "plh_pack_head"):
             getattr(L, n).restype = i32
         _bound = True
     return L
@@ -44,6 +50,20 @@ def transpose_block16(w_kv):
     out = np.empty((K // 8, V, 8), np.uint16)
     S._ok(lib().plh_transpose_block16(w.ctypes.data, out.ctypes.data, K, V), "plh_transpose_block16")
     return out
+
+
+def load_vocab_map(path, expected):
+    """plh_load_vocab_map: pruned-vocab/mapping.npy -> int32[expected]."""
+    out = np.zeros(int(expected), np.int32)
+    S._ok(lib().plh_load_vocab_map(str(path).encode(), int(expected), out.ctypes.data), "plh_load_vocab_map")
+    return out
+
+
+def pack_head(src_ptr, src_dtype, src_rows, K, mapping, V, w_bt_ptr, stream=None):
+    """plh_pack_head: device lm_head rows -> device block-transposed fp16 head."""
+    m = None if mapping is None else np.ascontiguousarray(mapping, np.int32)
+    S._ok(lib().plh_pack_head(src_ptr, src_dtype, src_rows, K, None if m is None else m.ctypes.data, V,
+                              w_bt_ptr, stream), "plh_pack_head")
 
 
 class LMHead:

@@ -13,7 +13,8 @@
                         patterns, getDataFP16(15001, 4096, 102400) at 64
                         (k, n) positions (the LM-head weights of the
                         validation run, src/validation.c:6174), and
-                        transpose_block16(QUANT_FP16) of a 16 x 5 matrix.
+                        transpose_block16(QUANT_FP16) of a 16 x 5 matrix,
+                        float_to_bf16 on the same 64 patterns.
 
 Run from the repository root:  python tests/golden/make_golden.py
 """
@@ -92,6 +93,8 @@ def fp16_fixture():
     ref.float_to_fp16.argtypes = [ctypes.c_float]
     ref.getDataFP16.restype = ctypes.c_void_p
     ref.getDataFP16.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    ref.float_to_bf16.restype = ctypes.c_uint16
+    ref.float_to_bf16.argtypes = [ctypes.c_float]
     ref.transpose_block16.restype = None
     ref.transpose_block16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
     libc = ctypes.CDLL(None)
@@ -112,10 +115,12 @@ def fp16_fixture():
     w = rng.integers(0, 65536, (16, 5), dtype=np.uint16)
     out = np.zeros(16 * 5, np.uint16)
     ref.transpose_block16(w.ctypes.data, out.ctypes.data, 16, 5, 16)
+    bbits = [int(ref.float_to_bf16(float(v))) for v in f]
     return {"float_to_fp16": {"in_bits": [int(b) for b in fbits], "out_bits": hbits},
+            "float_to_bf16": {"in_bits": [int(b) for b in fbits], "out_bits": bbits},
             "get_data_fp16": {"seed": 15001, "M": K, "N": V, "pos": pos, "bits": gvals},
             "transpose_block16": {"K": 16, "V": 5, "in": w.reshape(-1).tolist(), "out": out.tolist()},
-            "source": "reference src/data.c float_to_fp16 / getDataFP16 / transpose_block16, "
+            "source": "reference src/data.c float_to_fp16 / float_to_bf16 / getDataFP16 / transpose_block16, "
                       "compiled by oracle/Makefile"}
 
 

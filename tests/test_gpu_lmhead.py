@@ -7,7 +7,10 @@ greedy form against the oracle's argmax of those logits and against
 pss_enqueue(PSS_MODE_GREEDY) on plh_logits' output (same token, result slot,
 token_ids and position, nothing else touched); the reference validation case
 (src/validation.c:4893-4941: position 41 -> 42); ties, NaN weights and zero
-rows; two greedy calls in a row (the per-group tickets reset themselves)."""
+rows; two greedy calls in a row (the per-group tickets reset themselves);
+plh_pack_head against the reference's load-time build restated in the oracle
+(bf16 / fp16 rows, pruned by a map or not, format specials), then the logits of
+a packed head."""
 import numpy as np
 import pytest
 
@@ -234,3 +237,89 @@ def test_argument_errors():
         s_other.close()
         s_wrong_v.close()
         hd.close()
+
+
+def _src_rows(rng, rows, K, dtype):
+    bits = rng.integers(0, 65536, (rows, K), dtype=np.uint32).astype(np.uint16)
+    # specials of the source format: NaN, +-inf, zeros, subnormals, values past fp16's range
+    if dtype == L.SRC_FP16:
+        sp = [0x7E00, 0x7C00, 0xFC00, 0x0000, 0x8000, 0x0001, 0x03FF, 0x7BFF]
+    else:
+        sp = [0x7FC0, 0x7F80, 0xFF80, 0x0000, 0x8000, 0x0001, 0x477F, 0x4780, 0x3380]
+    flat = bits.reshape(-1)
+    n = min(len(sp), flat.size)
+    flat[:n] = sp[:n]
+    return bits
+
+
+@pytest.mark.parametrize("dtype", [0, 1], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("mapped", [True, False], ids=["pruned", "unpruned"])
+@pytest.mark.parametrize("K,V", [(24, 65), (264, 1000), (8, 1)])
+def test_pack_head_bit_exact(dtype, mapped, K, V):
+    rng = np.random.default_rng(K + V + 2 * dtype + mapped)
+    src_rows = V + 300 if mapped else V
+    src = _src_rows(rng, src_rows, K, dtype)
+    mapping = rng.permutation(src_rows)[:V].astype(np.int32) if mapped else None
+    if mapped:
+        mapping[:2] = [0, 1][:V]  # the rows holding the specials
+    want = O.pack_head(src, dtype, mapping)
+    print(f"pack_head dtype={dtype} mapped={mapped} K={K} V={V}", flush=True)
+    ds = hip.DeviceBuffer.from_array(src)
+    dw = hip.DeviceBuffer(K * V * 2)
+    try:
+        L.pack_head(ds.ptr, dtype, src_rows, K, mapping, V, dw.ptr)
+        got = dw.download(np.uint16, (K // 8, V, 8))
+    finally:
+        ds.free()
+        dw.free()
+    assert np.array_equal(got, want), np.argwhere(got != want)[:5]
+
+
+def test_pack_then_logits():
+    """bf16 lm_head rows of a 2,000-row vocabulary, pruned to 777 ids, packed on
+    the GPU, then plh_logits: the logits equal the oracle's on the oracle's
+    packed head."""
+    rng = np.random.default_rng(21)
+    K, V, src_rows = 256, 777, 2000
+    src = O.float_to_bf16(rng.normal(0, 0.05, (src_rows, K)).astype(np.float32))
+    mapping = rng.permutation(src_rows)[:V].astype(np.int32)
+    w_bt = O.pack_head(src, 0, mapping)
+    x = rng.normal(0, 2, (2, K)).astype(np.float32)
+    g = rng.normal(1, 0.2, K).astype(np.float32)
+    ds = hip.DeviceBuffer.from_array(src)
+    dw = hip.DeviceBuffer(K * V * 2)
+    dg, dx = hip.DeviceBuffer.from_array(g), hip.DeviceBuffer.from_array(x)
+    dl = hip.DeviceBuffer(2 * V * 4)
+    try:
+        L.pack_head(ds.ptr, 0, src_rows, K, mapping, V, dw.ptr)
+        h = L.LMHead(dw.ptr, dg.ptr, K, V, 2)
+        try:
+            h.logits(dx.ptr, K, 2, dl.ptr, V)
+            hip.stream_sync(h.stream)
+        finally:
+            h.close()
+        got = dl.download(np.float32, (2, V))
+    finally:
+        for b in (ds, dw, dg, dx, dl):
+            b.free()
+    assert _same(got, _oracle_logits(x, g, w_bt))
+
+
+def test_pack_head_errors():
+    src = np.zeros((10, 16), np.uint16)
+    ds = hip.DeviceBuffer.from_array(src)
+    dw = hip.DeviceBuffer(16 * 12 * 2)
+    try:
+        with pytest.raises(S.PssError):   # map entry past the source rows (src/prune.c:159-161)
+            L.pack_head(ds.ptr, 0, 10, 16, np.array([0, 10], np.int32), 2, dw.ptr)
+        with pytest.raises(S.PssError):   # negative entry
+            L.pack_head(ds.ptr, 0, 10, 16, np.array([-1], np.int32), 1, dw.ptr)
+        with pytest.raises(S.PssError):   # unpruned with fewer source rows than V
+            L.pack_head(ds.ptr, 0, 10, 16, None, 12, dw.ptr)
+        with pytest.raises(S.PssError):   # K % 8 != 0
+            L.pack_head(ds.ptr, 0, 10, 12, None, 10, dw.ptr)
+        with pytest.raises(S.PssError):   # source not 16-byte aligned
+            L.pack_head(ds.ptr + 2, 0, 9, 16, None, 9, dw.ptr)
+    finally:
+        ds.free()
+        dw.free()

@@ -170,3 +170,103 @@ def test_reference_validation_case():
     srt = np.sort(l64)
     err = max(np.abs(lo - l64).max(), np.abs(acc - l64).max())
     assert srt[-1] - srt[-2] > 20 * err
+
+
+def test_float_to_bf16_matches_reference_fixture():
+    f = np.array(FIX["float_to_bf16"]["in_bits"], np.uint32).view(np.float32)
+    assert O.float_to_bf16(f).tolist() == FIX["float_to_bf16"]["out_bits"]
+
+
+def test_float_to_bf16_rounds_to_nearest_even():
+    """Mathematical pin: the nearer of the two bf16 neighbours, the one with
+    an even last bit on a tie (finite values below the bf16 overflow)."""
+    rng = np.random.default_rng(11)
+    x = np.concatenate([rng.normal(0, 100, 20000), rng.uniform(-1e-30, 1e-30, 2000)]).astype(np.float32)
+    ties = (rng.integers(0, 1 << 16, 2000, dtype=np.uint32) << 16 | 0x8000).view(np.float32)
+    x = np.concatenate([x, ties[np.isfinite(ties)]])
+    b = x.view(np.uint32)
+    lo = (b & 0xFFFF0000).view(np.float32).astype(np.float64)
+    hi = ((b & 0xFFFF0000) + 0x10000).view(np.float32).astype(np.float64)
+    xd = x.astype(np.float64)
+    dlo, dhi = np.abs(xd - lo), np.abs(hi - xd)
+    lo_even = ((b >> 16) & 1) == 0
+    pick_lo = (dlo < dhi) | ((dlo == dhi) & lo_even)
+    want = np.where(pick_lo, b >> 16, (b >> 16) + 1).astype(np.uint16)
+    assert np.array_equal(O.float_to_bf16(x), want)
+
+
+def _ref_compose_pack(ref, src, dtype, mapping):
+    """The reference's own data.c functions composed as prune.c + weights.c do."""
+    import ctypes
+    ref.float_to_fp16.restype = ctypes.c_uint16
+    ref.float_to_fp16.argtypes = [ctypes.c_float]
+    ref.fp16_to_float.restype = ctypes.c_float
+    ref.fp16_to_float.argtypes = [ctypes.c_uint16]
+    ref.float_to_bf16.restype = ctypes.c_uint16
+    ref.float_to_bf16.argtypes = [ctypes.c_float]
+    ref.bf16_to_float.restype = ctypes.c_float
+    ref.bf16_to_float.argtypes = [ctypes.c_uint16]
+    ref.transpose_block16.restype = None
+    ref.transpose_block16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    rows = mapping if mapping is not None else np.arange(src.shape[0])
+    V, K = len(rows), src.shape[1]
+    eng = np.zeros((K, V), np.uint16)
+    for v, r in enumerate(rows):
+        for k in range(K):
+            raw = int(src[r, k])
+            if dtype == 0:
+                x = ref.bf16_to_float(raw)
+            elif mapping is not None:
+                x = ref.bf16_to_float(ref.float_to_bf16(ref.fp16_to_float(raw)))
+            else:
+                x = ref.fp16_to_float(raw)
+            eng[k, v] = ref.float_to_fp16(x)
+    out = np.zeros(K * V, np.uint16)
+    ref.transpose_block16(eng.ctypes.data, out.ctypes.data, K, V, 16)
+    return out
+
+
+@pytest.mark.parametrize("dtype,mapped", [(0, True), (1, True), (0, False), (1, False)])
+def test_pack_head_against_compiled_reference(dtype, mapped):
+    ref = O.ref_data_lib()
+    if ref is None:
+        pytest.skip("oracle/_ref not built (reference checkout absent)")
+    rng = np.random.default_rng(12 + dtype)
+    src = rng.integers(0, 65536, (40, 16), dtype=np.uint32).astype(np.uint16)
+    mapping = rng.integers(0, 40, 23).astype(np.int32) if mapped else None
+    want = _ref_compose_pack(ref, src, dtype, mapping)
+    assert np.array_equal(O.pack_head(src, dtype, mapping).reshape(-1), want)
+
+
+def test_load_vocab_map(tmp_path):
+    from pumice_amd import lmhead as L
+    from pumice_amd import sampler as S
+    m = np.random.default_rng(13).permutation(5000)[:1000].astype(np.int32)
+    p = tmp_path / "mapping.npy"
+    np.save(p, m)
+    assert np.array_equal(L.load_vocab_map(p, 1000), m)
+    with pytest.raises(S.PssError):
+        L.load_vocab_map(p, 999)                      # length mismatch
+    np.save(tmp_path / "i8.npy", m.astype(np.int64))
+    with pytest.raises(S.PssError):
+        L.load_vocab_map(tmp_path / "i8.npy", 1000)   # not int32
+    with open(tmp_path / "v2.npy", "wb") as f:
+        np.lib.format.write_array(f, m, version=(2, 0))
+    with pytest.raises(S.PssError):
+        L.load_vocab_map(tmp_path / "v2.npy", 1000)   # only version 1, as the reference
+    (tmp_path / "bad.npy").write_bytes(b"NOTNPY" + bytes(200))
+    with pytest.raises(S.PssError):
+        L.load_vocab_map(tmp_path / "bad.npy", 1000)
+    with pytest.raises(S.PssError):
+        L.load_vocab_map(tmp_path / "missing.npy", 1000)
+
+
+def test_reference_mapping_file():
+    path = "/root/reference/pruned-vocab/mapping.npy"
+    if not os.path.exists(path):
+        pytest.skip("reference checkout absent")
+    from pumice_amd import lmhead as L
+    m = L.load_vocab_map(path, 102400)
+    want = np.load(path, allow_pickle=False)
+    assert want.dtype == np.int32 and np.array_equal(m, want)
+    assert m.min() >= 0 and m.max() < 248320 and np.unique(m).size == m.size
