@@ -227,6 +227,21 @@ def bench_lmhead(steps, K=4096, V=102400, rows_list=(1, 4)):
                 out[f"{name}_rows{rows}_us"] = us
                 out[f"{name}_rows{rows}_gbps"] = nbytes / (us * 1e-6) / 1e9
         out["logits_rows1_frac"] = out["logits_rows1_gbps"] / HBM_PEAK_GBPS
+        # load-time build of this head from a 248,320-row bf16 lm_head pruned
+        # to V ids (plh_pack_head: gather + conversions + block transpose)
+        src_rows = 248320
+        src = hip.DeviceBuffer(src_rows * K * 2)
+        try:
+            mapping = np.sort(rng.permutation(src_rows)[:V]).astype(np.int32)
+            L.pack_head(src.ptr, L.SRC_BF16, src_rows, K, mapping, V, dw.ptr)  # warm
+            t0 = time.perf_counter()
+            for _ in range(3):
+                L.pack_head(src.ptr, L.SRC_BF16, src_rows, K, mapping, V, dw.ptr)
+            us = (time.perf_counter() - t0) / 3 * 1e6
+            out["pack_head_us"] = us
+            out["pack_head_gbps"] = 2 * K * V * 2 / (us * 1e-6) / 1e9
+        finally:
+            src.free()
     finally:
         s.close()
         head.close()
