@@ -20,6 +20,8 @@ A "step" is one pss_enqueue over a batch of logit rows resident in HBM.
   lmhead    the LM head before the sampler (RMSNorm + fp16 GEMV over a
             4,096 x 102,400 block-transposed head): us per call and HBM GB/s
             for 1 and 4 rows, logits and fused-greedy forms.
+  read ceiling  a plain streaming read of one headline batch (torch.sum) on
+            the same box, for comparison with the kernels' HBM rates.
   cpu_baseline  the O1 oracle (scalar C, sort-based) on the box's host cores
             over a bounded sample of the headline rows.
 
@@ -250,6 +252,29 @@ def bench_lmhead(steps, K=4096, V=102400, rows_list=(1, 4)):
     return out
 
 
+def read_ceiling(nbytes, reps=50):
+    """Achievable read bandwidth on this box: torch's sum over a rotating
+    set of fp32 tensors of `nbytes` each (plain loads, beyond the last-level
+    cache), timed with torch events on torch's stream."""
+    import torch
+
+    n = nbytes // 4
+    xs = [torch.ones(n, dtype=torch.float32, device="cuda") for _ in range(NBUF)]
+    for i in range(5):
+        xs[i % NBUF].sum()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(reps):
+        xs[i % NBUF].sum()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    del xs
+    torch.cuda.empty_cache()
+    return {"bytes": nbytes, "us": us, "gbps": nbytes / (us * 1e-6) / 1e9, "how": "torch.sum, fp32, 6 rotating buffers"}
+
+
 def cpu_baseline(w, seconds):
     """O1 (scalar C, sort-based restatement) on a bounded sample of the headline rows."""
     import oracle as O
@@ -423,6 +448,11 @@ def main():
         log("lm head (K 4096 x V 102400)")
         extra["lmhead"] = bench_lmhead(args.lmhead_steps)
         log("lmhead", json.dumps(extra["lmhead"]))
+        try:
+            extra["read_ceiling"] = read_ceiling(head.logits.nbytes)
+            log("read ceiling", json.dumps(extra["read_ceiling"]))
+        except Exception as exc:  # torch without a device build: no ceiling line
+            log("read ceiling unavailable:", exc)
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
