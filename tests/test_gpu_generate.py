@@ -192,3 +192,18 @@ def test_closed_gate_changes_nothing(flags):
         s.close()
         dev.free()
         pb.free()
+
+
+@pytest.mark.parametrize("max_new", [1, 2, 5, 6])
+def test_pipelined_short_runs(max_new):
+    """Prefill only, one partial group, one full group, one full group plus a
+    pass: the pipelined loop equals the unpipelined one (tokens, slots, state)."""
+    xs, params, hist = _inputs(25)
+    ref, _ = _oracle_chain(xs, params, hist, S.RNG_XORSHIFT32, max_new)
+    a = _run_loop(xs, params, hist, 1, 0xFFFFFFFF, max_new, "readback")
+    b = _run_loop(xs, params, hist, 1, 0xFFFFFFFF, max_new, "pipelined")
+    assert a[0] == b[0] == ref
+    assert a[1]["groups"] == b[1]["groups"] == (max_new - 1 + 3) // 4
+    assert np.array_equal(a[2], b[2]) and np.array_equal(a[3], b[3])
+    for k in ("history", "position", "rng", "step"):
+        assert np.array_equal(a[4][k], b[4][k]), k
