@@ -19,9 +19,9 @@
  *                     vector side issues only the weight loads, 8 fp16->fp32
  *                     conversions and 8 R fused multiply-adds per block.  The
  *                     four slice partials meet in LDS and are added in slice
- *                     order.  The head is read once per row group (R rows
- *                     share each weight load): the kernel is bound by HBM, the
- *                     algorithmic bytes are K V 2 per group.
+ *                     order.  The head is read once per row group (R = 1, 2,
+ *                     4 or 8 rows share each weight load): the kernel is
+ *                     bound by HBM, the algorithmic bytes are K V 2 per group.
  *
  * Greedy form: each workgroup reduces its 64 columns to the packed maximum
  * (key(value) << 32) | (0xFFFFFFFF - id) (largest value, then lowest id; NaN
@@ -49,6 +49,7 @@
 static_assert(PLH_NT == PLH_SLICES * PSS_WAVE, "one wave per K-slice");
 static_assert(PLH_TILE == PSS_WAVE, "one column per lane");
 static_assert(PLH_WIN_SLOTS == 16u, "the final reduction reads the slots with 16 lanes per row");
+static_assert(16u * 8u <= PLH_NT, "16 lanes per row of a group");
 
 struct plh_head {
     int device;
@@ -335,8 +336,10 @@ extern "C" pss_status plh_destroy(plh_head* h) {
 
 extern "C" void* plh_stream(plh_head* h) { return h ? (void*)h->stream : NULL; }
 
-/* Rows per weight pass: 1, 2, or groups of 4. */
-static inline int plh_pick_r(uint32_t rows) { return rows == 1u ? 1 : rows == 2u ? 2 : 4; }
+/* Rows per weight pass: 1, 2, 4 (3 or 4 rows), or groups of 8 (VALU work per
+ * 16-byte block: 8 conversions folded into 8 R fused multiply-adds, still
+ * under the block's HBM time at 8 rows; 16 would be VALU-bound). */
+static inline int plh_pick_r(uint32_t rows) { return rows == 1u ? 1 : rows == 2u ? 2 : rows <= 4u ? 4 : 8; }
 
 template <bool GREEDY>
 static pss_status plh_launch(plh_head* h, const float* x, uint64_t xs, uint32_t rows, plh_args a) {
@@ -347,8 +350,10 @@ static pss_status plh_launch(plh_head* h, const float* x, uint64_t xs, uint32_t 
         hipLaunchKernelGGL((plh_gemv_kernel<1, GREEDY>), grid, dim3(PLH_NT), 0, h->stream, a, (const float*)h->an);
     else if (R == 2)
         hipLaunchKernelGGL((plh_gemv_kernel<2, GREEDY>), grid, dim3(PLH_NT), 0, h->stream, a, (const float*)h->an);
-    else
+    else if (R == 4)
         hipLaunchKernelGGL((plh_gemv_kernel<4, GREEDY>), grid, dim3(PLH_NT), 0, h->stream, a, (const float*)h->an);
+    else
+        hipLaunchKernelGGL((plh_gemv_kernel<8, GREEDY>), grid, dim3(PLH_NT), 0, h->stream, a, (const float*)h->an);
     return hipGetLastError() == hipSuccess ? PSS_OK : PSS_ERR_HIP;
 }
 
