@@ -26,8 +26,8 @@
  * Greedy form: each workgroup reduces its 64 columns to the packed maximum
  * (key(value) << 32) | (0xFFFFFFFF - id) (largest value, then lowest id; NaN
  * maps to -inf) and folds it into one of the row's PLH_WIN_SLOTS slots (tile
- * mod 16, each in its own 128-byte line, so the atomics of 1,600 workgroups
- * of a 102,400-column head do not queue on one address) with an agent-scope atomic max; it waits for
+ * mod 64, each in its own 128-byte line, so the atomics of 1,600 workgroups
+ * of a 102,400-column head, which finish together, queue 25 deep at most) with an agent-scope atomic max; it waits for
  * the atomic and counts itself on the row group's ticket.  The workgroup that
  * completes the count resets the ticket, reads and clears the slots, and
  * writes result / token_ids / position as ArgMax-Reduce mode 0.
@@ -42,13 +42,13 @@
 #include "pumice_lmhead.h"
 
 #define PLH_NORM_NT 256
-#define PLH_WIN_SLOTS 16u
+#define PLH_WIN_SLOTS 64u
 #define PLH_WIN_STRIDE 16u /* u64 per slot: one 128-byte line */
 #define PLH_WIN_ROW (PLH_WIN_SLOTS * PLH_WIN_STRIDE)
 #define PLH_NT 256 /* PLH_SLICES waves */
 static_assert(PLH_NT == PLH_SLICES * PSS_WAVE, "one wave per K-slice");
 static_assert(PLH_TILE == PSS_WAVE, "one column per lane");
-static_assert(PLH_WIN_SLOTS == 16u, "the final reduction reads the slots with 16 lanes per row");
+static_assert(PLH_WIN_SLOTS == PSS_WAVE, "the final reduction reads a row's slots with one wave");
 static_assert(16u * 8u <= PLH_NT, "16 lanes per row of a group");
 
 struct plh_head {
@@ -244,20 +244,15 @@ __global__ void __launch_bounds__(PLH_NT) plh_gemv_kernel(plh_args a, const floa
     if constexpr (GREEDY) {
         __syncthreads();
         if (!last) return;
-        if (tid < 16u * (uint32_t)R) {
-            const uint32_t row = g * (uint32_t)R + (tid >> 4);
-            uint64_t best = 0;
-            if (row < a.rows) {
-                unsigned long long* p = &a.win[(size_t)row * PLH_WIN_ROW + (tid & 15u) * PLH_WIN_STRIDE];
-                best = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(p, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-#pragma unroll
-            for (int off = 8; off >= 1; off >>= 1) {
-                const uint64_t o = __shfl_xor(best, off, 16);
-                best = o > best ? o : best;
-            }
-            if ((tid & 15u) == 0u && row < a.rows) {
+        /* wave w reduces rows w, w + 4, ... of the group: lane = slot */
+        for (uint32_t r = tid >> 6; r < (uint32_t)R; r += PLH_NT / PSS_WAVE) {
+            const uint32_t row = g * (uint32_t)R + r;
+            if (row >= a.rows) break;
+            unsigned long long* p = &a.win[(size_t)row * PLH_WIN_ROW + lane * PLH_WIN_STRIDE];
+            uint64_t best = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(p, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            best = wave_max_u64(best);
+            if (lane == 0u) {
                 const uint32_t tok = 0xFFFFFFFFu - (uint32_t)best;
                 a.result[row * PSS_RESULT_SLOTS + a.pass_idx] = tok;
                 a.token_ids[row] = tok;
