@@ -20,8 +20,9 @@ A "step" is one pss_enqueue over a batch of logit rows resident in HBM.
   lmhead    the LM head before the sampler (RMSNorm + fp16 GEMV over a
             4,096 x 102,400 block-transposed head): us per call and HBM GB/s
             for 1 and 4 rows, logits and fused-greedy forms.
-  read ceiling  a plain streaming read of one headline batch (torch.sum) on
-            the same box, for comparison with the kernels' HBM rates.
+  torch_sum_same_bytes  a library reduction (torch.sum, fp32) over the
+            same bytes as one headline batch, on the same box, for context
+            beside the kernels' HBM rates (run in a child process).
   cpu_baseline  the O1 oracle (scalar C, sort-based) on the box's host cores
             over a bounded sample of the headline rows.
 
@@ -252,27 +253,37 @@ def bench_lmhead(steps, K=4096, V=102400, rows_list=(1, 4)):
     return out
 
 
-def read_ceiling(nbytes, reps=50):
-    """Achievable read bandwidth on this box: torch's sum over a rotating
-    set of fp32 tensors of `nbytes` each (plain loads, beyond the last-level
-    cache), timed with torch events on torch's stream."""
-    import torch
+_READ_CEILING = r"""
+import json, sys, torch
+nbytes, reps, nbuf = int(sys.argv[1]), int(sys.argv[2]), int(sys.argv[3])
+xs = [torch.ones(nbytes // 4, dtype=torch.float32, device="cuda") for _ in range(nbuf)]
+for i in range(5):
+    xs[i % nbuf].sum()
+torch.cuda.synchronize()
+e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+e0.record()
+for i in range(reps):
+    xs[i % nbuf].sum()
+e1.record()
+torch.cuda.synchronize()
+us = e0.elapsed_time(e1) * 1e3 / reps
+print(json.dumps({"bytes": nbytes, "us": us, "gbps": nbytes / (us * 1e-6) / 1e9,
+                  "how": "torch.sum over fp32, %d rotating buffers, child process" % nbuf}))
+"""
 
-    n = nbytes // 4
-    xs = [torch.ones(n, dtype=torch.float32, device="cuda") for _ in range(NBUF)]
-    for i in range(5):
-        xs[i % NBUF].sum()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for i in range(reps):
-        xs[i % NBUF].sum()
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / reps
-    del xs
-    torch.cuda.empty_cache()
-    return {"bytes": nbytes, "us": us, "gbps": nbytes / (us * 1e-6) / 1e9, "how": "torch.sum, fp32, 6 rotating buffers"}
+
+def read_ceiling(nbytes, reps=50):
+    """torch's sum over a rotating set of fp32 tensors of `nbytes` each
+    (beyond the last-level cache), timed with torch events, in a child
+    process (torch brings its own HIP runtime, which does not share a process
+    with this library's)."""
+    import subprocess
+
+    r = subprocess.run([sys.executable, "-c", _READ_CEILING, str(nbytes), str(reps), str(NBUF)],
+                       capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        raise RuntimeError(r.stderr.strip().splitlines()[-1] if r.stderr.strip() else "child failed")
+    return json.loads(r.stdout.strip().splitlines()[-1])
 
 
 def cpu_baseline(w, seconds):
@@ -449,10 +460,10 @@ def main():
         extra["lmhead"] = bench_lmhead(args.lmhead_steps)
         log("lmhead", json.dumps(extra["lmhead"]))
         try:
-            extra["read_ceiling"] = read_ceiling(head.logits.nbytes)
-            log("read ceiling", json.dumps(extra["read_ceiling"]))
-        except Exception as exc:  # torch without a device build: no ceiling line
-            log("read ceiling unavailable:", exc)
+            extra["torch_sum_same_bytes"] = read_ceiling(head.logits.nbytes)
+            log("torch.sum over one batch", json.dumps(extra["torch_sum_same_bytes"]))
+        except Exception as exc:  # torch without a device build: no line
+            log("torch.sum baseline unavailable:", exc)
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
