@@ -7,8 +7,8 @@
  * wave's LDS staging area, one round ahead of its compute; window ids are
  * applied once per id by the lane that claims them; every element at or
  * above a certified lower bound of the row's K-th largest value (from the
- * waves' running top values, combined across the workgroup after the round's
- * one barrier) becomes a candidate.  Two forms:
+ * waves' running top values, combined across the workgroup through LDS
+ * slots) becomes a candidate.  Two forms:
  *
  * pss_row_kernel (default), one workgroup per row: candidates gather in an
  * LDS list and the workgroup finishes the row itself after its last round --
@@ -1145,20 +1145,29 @@ __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, u
                                             pss_key(pss_canon(t3))};
                     T = pss_wave_kth16<4>(k4, kq);
                 }
-                if (lane == 0u) joint[wave] = ((unsigned long long)row << 32) | T;
+                if (lane == 0u)
+                    __hip_atomic_store(&joint[wave], ((unsigned long long)row << 32) | T, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
             }
         } else if (ncov) {
             pss_wave_issue<EPT, DT, FUSED ? PSS_NT : 0>(a, nrow, ns, wl);
             pss_wave_side_load(a, nrow, nsp, nsd, !FUSED);
         }
-        __syncthreads();
+        /* The joint certificate needs every slot written once (round 0's
+         * barrier).  In the fused form every slot belongs to this row, and a
+         * slot only ever grows: whatever mix of this round's and earlier
+         * rounds' slots a wave reads, each slot still certifies its own
+         * ceil(K / 16) elements, so later rounds need no barrier and a wave
+         * whose item arrived early does not wait for the slowest one
+         * (slot accesses are atomic 64-bit LDS accesses). */
+        if (!FUSED || r == 0u) __syncthreads();
 
         /* ---- B ---- */
         if (cov && !greedy) {
             const pss_rowcfg& c = run.c;
             pss_row_ws* ws = (pss_row_ws*)((char*)a.ws + (size_t)row * PSS_WS_ROW_BYTES);
             /* joint certificate: all NW slots on this row */
-            const unsigned long long e = joint[lane % NW];
+            const unsigned long long e = __hip_atomic_load(&joint[lane % NW], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             const bool bad = (uint32_t)(e >> 32) != row;
             uint32_t L = 0u;
             if (__ballot(bad) == 0ull) {
