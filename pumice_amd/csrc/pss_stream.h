@@ -1159,8 +1159,10 @@ __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, u
          * rounds' slots a wave reads, each slot still certifies its own
          * ceil(K / 16) elements, so later rounds need no barrier and a wave
          * whose item arrived early does not wait for the slowest one
-         * (slot accesses are atomic 64-bit LDS accesses). */
-        if (!FUSED || r == 0u) __syncthreads();
+         * (slot accesses are atomic 64-bit LDS accesses).  The wide form
+         * keeps the barrier: at top-k up to 1,024 a certificate one round
+         * old lets measurably more candidates into its list. */
+        if (!FUSED || WL || r == 0u) __syncthreads();
 
         /* ---- B ---- */
         if (cov && !greedy) {
