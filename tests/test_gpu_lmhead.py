@@ -10,7 +10,7 @@ token_ids and position, nothing else touched); the reference validation case
 rows; two greedy calls in a row (the per-group tickets reset themselves);
 plh_pack_head against the reference's load-time build restated in the oracle
 (bf16 / fp16 rows, pruned by a map or not, format specials), then the logits of
-a packed head."""
+a packed head; 12 seeded random shapes, strides and scales (logits and greedy)."""
 import numpy as np
 import pytest
 
@@ -323,3 +323,45 @@ def test_pack_head_errors():
     finally:
         ds.free()
         dw.free()
+
+
+def _random_head_case(seed):
+    rng = np.random.default_rng(500 + seed)
+    K = 8 * int(rng.integers(1, 513))
+    V = int(rng.integers(1, 40001))
+    rows = int(rng.integers(1, 9))
+    x = (rng.normal(0, rng.uniform(0.01, 10.0), (rows, K))).astype(np.float32)
+    if rows > 1 and rng.random() < 0.3:
+        x[int(rng.integers(0, rows))] = 0.0             # a zero row: every logit 0, token 0
+    g = rng.normal(1, rng.uniform(0.0, 1.0), K).astype(np.float32)
+    if rng.random() < 0.3:                               # few distinct weights: tied logits
+        w = rng.integers(-3, 4, (K, V)).astype(np.float32) * np.float32(0.125)
+    else:
+        w = rng.normal(0, rng.uniform(0.001, 2.0), (K, V)).astype(np.float32)
+    return x, g, O.float_to_fp16(w)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_heads(seed):
+    """Seeded random shapes (K from 8 to 4,096, V from 1 to 40,000, 1..8 rows),
+    padded strides, activation and weight scales over several decades, tied
+    and zero rows: logits bit-exact, then the fused greedy form's tokens."""
+    x, g, w_kv = _random_head_case(seed)
+    rows, K = x.shape
+    V = w_kv.shape[1]
+    rng = np.random.default_rng(seed)
+    x_stride = K + 4 * int(rng.integers(0, 3))
+    l_stride = V + int(rng.integers(0, 5))
+    print(f"lmhead random {seed}: K={K} V={V} rows={rows} strides {x_stride}/{l_stride}", flush=True)
+    w_bt = O.transpose_block16(w_kv)
+    want = _oracle_logits(x, g, w_bt)
+    hd = _Head(x, g, w_bt, x_stride=x_stride)
+    try:
+        got = hd.logits(stride=l_stride)
+    finally:
+        hd.close()
+    assert _same(got[:, :V], want)
+    res, tok, before, after = _greedy_run(x, g, w_bt, pass_idx=1)
+    assert [int(t) for t in tok] == [O.greedy(want[r]) for r in range(rows)]
+    assert [int(r[1]) for r in res] == [int(t) for t in tok]
+    assert np.array_equal(after["position"], before["position"] + 1)
