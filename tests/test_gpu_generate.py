@@ -207,3 +207,29 @@ def test_pipelined_short_runs(max_new):
     assert np.array_equal(a[2], b[2]) and np.array_equal(a[3], b[3])
     for k in ("history", "position", "rng", "step"):
         assert np.array_equal(a[4][k], b[4][k]), k
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_random_decode_runs(seed):
+    """Seeded random runs: 1..8 rows, 1..40 new tokens, either rng mode, EOS at
+    a random point of the chain or never.  The three loops (slots read back per
+    group, pinned tokens, pipelined) give the oracle chain's tokens, the same
+    finish and the same result slots, token ids and final state."""
+    rng = np.random.default_rng(300 + seed)
+    rows = int(rng.integers(1, 9))
+    max_new = int(rng.integers(1, 41))
+    rng_mode = S.RNG_PHILOX if rng.random() < 0.5 else S.RNG_XORSHIFT32
+    xs, params, hist = _inputs(100 + seed)
+    ref, _ = _oracle_chain(xs, params, hist, rng_mode, max_new)
+    idx = int(rng.integers(0, max_new)) if rng.random() < 0.6 else None
+    eos = ref[idx] if idx is not None else 0xFFFFFFFF
+    print(f"random decode {seed}: rows={rows} max_new={max_new} eos_index={idx}", flush=True)
+    runs = [_run_loop(xs, params, hist, rows, eos, max_new, loop, rng_mode) for loop in LOOPS]
+    a = runs[0]
+    assert a[0] == ref[:len(a[0])]
+    for b in runs[1:]:
+        assert a[0] == b[0]
+        assert a[1]["emitted"] == b[1]["emitted"] and a[1]["finish_reason"] == b[1]["finish_reason"]
+        assert np.array_equal(a[2], b[2]) and np.array_equal(a[3], b[3])
+        for k in ("history", "position", "rng", "step"):
+            assert np.array_equal(a[4][k], b[4][k]), k
