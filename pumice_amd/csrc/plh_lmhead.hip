@@ -27,10 +27,12 @@
  * (key(value) << 32) | (0xFFFFFFFF - id) (largest value, then lowest id; NaN
  * maps to -inf) and folds it into one of the row's PLH_WIN_SLOTS slots (tile
  * mod 64, each in its own 128-byte line, so the atomics of 1,600 workgroups
- * of a 102,400-column head, which finish together, queue 25 deep at most) with an agent-scope atomic max; it waits for
- * the atomic and counts itself on the row group's ticket.  The workgroup that
- * completes the count resets the ticket, reads and clears the slots, and
- * writes result / token_ids / position as ArgMax-Reduce mode 0.
+ * of a 102,400-column head, which finish together, queue 25 deep at most) with an agent-scope atomic max and
+ * ends: no workgroup waits for its atomic.  plh_greedy_reduce_kernel, next on
+ * the stream (the kernel boundary orders the atomics before its loads), reads
+ * and clears a row's slots with one wave and writes result / token_ids /
+ * position as ArgMax-Reduce mode 0 -- the reference's own two dispatches
+ * (src/generate.c:540-546).
  */
 #include <hip/hip_runtime.h>
 #include <stdlib.h>
@@ -60,7 +62,6 @@ struct plh_head {
     uint32_t K, V, max_rows, ntiles;
     float* an;               /* [max_rows][K] normalized rows */
     unsigned long long* win; /* [max_rows][PLH_WIN_ROW] greedy maxima, zero between calls */
-    uint32_t* tickets;       /* [max_rows] row-group tickets, zero between calls */
 };
 
 struct plh_args {
@@ -68,7 +69,6 @@ struct plh_args {
     float* logits;
     uint64_t lstride;
     unsigned long long* win;
-    uint32_t* tickets;
     uint32_t* result;
     uint32_t* token_ids;
     uint32_t* position;
@@ -185,7 +185,6 @@ __device__ __forceinline__ void plh_consume(const uint4 (&q)[N], const float* co
 template <int R, bool GREEDY>
 __global__ void __launch_bounds__(PLH_NT) plh_gemv_kernel(plh_args a, const float* __restrict__ an) {
     __shared__ float part[PLH_SLICES][R][PSS_WAVE];
-    __shared__ uint32_t last;
     const uint32_t tile = blockIdx.x, g = blockIdx.y;
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t s = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -214,9 +213,7 @@ __global__ void __launch_bounds__(PLH_NT) plh_gemv_kernel(plh_args a, const floa
 #pragma unroll
     for (int r = 0; r < R; ++r) part[s][r][lane] = acc[r];
     __syncthreads();
-    if (s != 0u) {
-        if (!GREEDY) return;
-    } else {
+    if (s == 0u) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             float v = part[0][r][lane];
@@ -233,32 +230,22 @@ __global__ void __launch_bounds__(PLH_NT) plh_gemv_kernel(plh_args a, const floa
                                                  (unsigned long long)best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
-        if (!GREEDY) return;
-        pss_wait_mem(); /* this wave's atomics have been performed */
-        if (lane == 0u) {
-            const bool l = atomicAdd(&a.tickets[g], 1u) == gridDim.x - 1u;
-            if (l) __hip_atomic_store(&a.tickets[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last = l ? 1u : 0u;
-        }
     }
-    if constexpr (GREEDY) {
-        __syncthreads();
-        if (!last) return;
-        /* wave w reduces rows w, w + 4, ... of the group: lane = slot */
-        for (uint32_t r = tid >> 6; r < (uint32_t)R; r += PLH_NT / PSS_WAVE) {
-            const uint32_t row = g * (uint32_t)R + r;
-            if (row >= a.rows) break;
-            unsigned long long* p = &a.win[(size_t)row * PLH_WIN_ROW + lane * PLH_WIN_STRIDE];
-            uint64_t best = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(p, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            best = wave_max_u64(best);
-            if (lane == 0u) {
-                const uint32_t tok = 0xFFFFFFFFu - (uint32_t)best;
-                a.result[row * PSS_RESULT_SLOTS + a.pass_idx] = tok;
-                a.token_ids[row] = tok;
-                if (a.do_inc) a.position[row] = a.position[row] + 1u;
-            }
-        }
+}
+
+/* Greedy form, second kernel: one wave per row, lane = slot; the row's token
+ * is the lowest id among its largest logits (0xFFFFFFFF - the packed
+ * maximum's low half).  Every slot is cleared for the next call. */
+__global__ void __launch_bounds__(PSS_WAVE) plh_greedy_reduce_kernel(plh_args a) {
+    const uint32_t row = blockIdx.x, lane = threadIdx.x;
+    unsigned long long* p = &a.win[(size_t)row * PLH_WIN_ROW + lane * PLH_WIN_STRIDE];
+    const uint64_t best = wave_max_u64(*p);
+    *p = 0ull;
+    if (lane == 0u) {
+        const uint32_t tok = 0xFFFFFFFFu - (uint32_t)best;
+        a.result[row * PSS_RESULT_SLOTS + a.pass_idx] = tok;
+        a.token_ids[row] = tok;
+        if (a.do_inc) a.position[row] = a.position[row] + 1u;
     }
 }
 
@@ -270,7 +257,6 @@ static void plh_free(plh_head* h) {
     if (!h) return;
     if (h->an) (void)hipFree(h->an);
     if (h->win) (void)hipFree(h->win);
-    if (h->tickets) (void)hipFree(h->tickets);
     if (h->own_stream && h->stream) (void)hipStreamDestroy(h->stream);
     free(h);
 }
@@ -307,13 +293,11 @@ extern "C" pss_status plh_create(plh_head** out, const void* weight_bt, const fl
         h->own_stream = 1;
     }
     if (hipMalloc((void**)&h->an, (size_t)max_rows * K * 4u) != hipSuccess ||
-        hipMalloc((void**)&h->win, (size_t)max_rows * PLH_WIN_ROW * 8u) != hipSuccess ||
-        hipMalloc((void**)&h->tickets, (size_t)max_rows * 4u) != hipSuccess) {
+        hipMalloc((void**)&h->win, (size_t)max_rows * PLH_WIN_ROW * 8u) != hipSuccess) {
         plh_free(h);
         return PSS_ERR_ALLOC;
     }
-    if (hipMemsetAsync(h->tickets, 0, (size_t)max_rows * 4u, h->stream) != hipSuccess ||
-        hipMemsetAsync(h->win, 0, (size_t)max_rows * PLH_WIN_ROW * 8u, h->stream) != hipSuccess ||
+    if (hipMemsetAsync(h->win, 0, (size_t)max_rows * PLH_WIN_ROW * 8u, h->stream) != hipSuccess ||
         hipStreamSynchronize(h->stream) != hipSuccess) {
         plh_free(h);
         return PSS_ERR_HIP;
@@ -349,6 +333,7 @@ static pss_status plh_launch(plh_head* h, const float* x, uint64_t xs, uint32_t 
         hipLaunchKernelGGL((plh_gemv_kernel<4, GREEDY>), grid, dim3(PLH_NT), 0, h->stream, a, (const float*)h->an);
     else
         hipLaunchKernelGGL((plh_gemv_kernel<8, GREEDY>), grid, dim3(PLH_NT), 0, h->stream, a, (const float*)h->an);
+    if (GREEDY) hipLaunchKernelGGL(plh_greedy_reduce_kernel, dim3(rows), dim3(PSS_WAVE), 0, h->stream, a);
     return hipGetLastError() == hipSuccess ? PSS_OK : PSS_ERR_HIP;
 }
 
@@ -357,7 +342,6 @@ static plh_args plh_make_args(const plh_head* h, uint32_t rows) {
     memset(&a, 0, sizeof(a));
     a.w = h->w;
     a.win = h->win;
-    a.tickets = h->tickets;
     a.K = h->K;
     a.V = h->V;
     a.rows = rows;
