@@ -27,6 +27,9 @@
 
 enum { PLP_CONV_BF16 = 0, PLP_CONV_FP16_VIA_BF16 = 1, PLP_CONV_FP16 = 2 };
 
+/* Source and head are each touched once: nontemporal loads and stores. */
+typedef unsigned int plp_u32x4 __attribute__((ext_vector_type(4)));
+
 /* src/data.c:30-52 float_to_fp16: truncation, no rounding; e < -24 -> signed
  * zero, e <= -15 -> subnormal (mantissa with its hidden bit shifted right by
  * -1 - e), e >= 16 -> signed infinity (NaN included). */
@@ -79,7 +82,7 @@ __global__ void __launch_bounds__(PLP_NT) plh_pack_kernel(const uint4* __restric
         uint4 v = make_uint4(0u, 0u, 0u, 0u);
         if (n < V && kb < KB) {
             const uint32_t row = map ? (uint32_t)map[n] : n;
-            const uint4 q = src[(size_t)row * KB + kb];
+            const plp_u32x4 q = __builtin_nontemporal_load((const plp_u32x4*)&src[(size_t)row * KB + kb]);
             const uint32_t w[4] = {q.x, q.y, q.z, q.w};
             uint32_t o[4];
 #pragma unroll
@@ -94,7 +97,11 @@ __global__ void __launch_bounds__(PLP_NT) plh_pack_kernel(const uint4* __restric
     for (uint32_t pass = 0; pass < PLP_TN * PLP_TKB / PLP_NT; ++pass) {
         const uint32_t b = pass * (PLP_NT / PLP_TN) + t / PLP_TN, r = t % PLP_TN;
         const uint32_t n = n0 + r, kb = kb0 + b;
-        if (n < V && kb < KB) out[(size_t)kb * V + n] = tile[r][b];
+        if (n < V && kb < KB) {
+            const uint4 v = tile[r][b];
+            const plp_u32x4 o = {v.x, v.y, v.z, v.w};
+            __builtin_nontemporal_store(o, (plp_u32x4*)&out[(size_t)kb * V + n]);
+        }
     }
 }
 
