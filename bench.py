@@ -8,8 +8,9 @@ A "step" is one pss_enqueue over a batch of logit rows resident in HBM.
             sampled rows/s, plus algorithmic HBM GB/s and its roofline
             fraction.  Each step reads a different one of NBUF batches, so the
             working set (>= 600 MB) exceeds the 256 MB last-level cache and
-            rows come from HBM.  One step is one launch of pss_row_kernel (or, with
-            --split / --general, the other two forms).
+            rows come from HBM.  One step is one launch of pss_res_kernel (the
+            register-resident form; --fused / --split / --general force the
+            other forms).
   latency   batch 1 (config c2; the small-batch form, pss_small_kernel):
             launch-to-token p50/p90 (host clock, token stored by the kernel
             into pinned host memory), per-step GPU time, and steady
@@ -69,7 +70,7 @@ def copy_calibration(nbytes, reps=10):
 def bench_batched(w, steps, warmup, flags=0):
     """rows/s and per-launch GPU time for workload `w` (rows x V).
 
-    The default path is one kernel per step (pss_row_kernel); with
+    The default path is one kernel per step (pss_res_kernel); with
     S.ENQ_SPLIT it is two (pss_seg_kernel, then pss_fin_kernel) and the split
     event the library records between them times each one."""
     from pumice_amd import hip
@@ -322,7 +323,7 @@ def _cpu_model():
     return "unknown"
 
 
-def traffic_from_pmc(fetch_dir, write_dir, out_path):
+def traffic_from_pmc(fetch_dir, write_dir, out_path, kname="pss_res_kernel"):
     """HBM bytes per launch of the sampler kernels from two rocprofv3 --pmc runs
     of `bench.py --no-extra --no-cpu-baseline --copy-calib` (FETCH_SIZE, then
     WRITE_SIZE; counters in KiB per dispatch).  Each counter is scaled by what it
@@ -350,15 +351,15 @@ def traffic_from_pmc(fetch_dir, write_dir, out_path):
         scale = nbytes / (float(np.mean(copy)) * 1024.0)
         out[counter] = {"copy_kib": float(np.mean(copy)), "scale": scale}
         for (k, g), vs in vals.items():
-            if "pss_row_kernel" in k:
+            if kname in k:
                 out[counter]["row_kib"] = float(np.mean(vs))
                 out[counter]["row_bytes"] = float(np.mean(vs)) * 1024.0 * scale
     row = out["FETCH_SIZE"]["row_bytes"] + out["WRITE_SIZE"]["row_bytes"]
-    res = {"workload": "headline 256 x 102,400 fp32", "calibration_copy_bytes": nbytes,
+    res = {"kernel": kname, "workload": "headline 256 x 102,400 fp32", "calibration_copy_bytes": nbytes,
            "counters": out, "row_kernel_hbm_bytes_per_launch": row}
     fc, wc = out["FETCH_SIZE"], out["WRITE_SIZE"]
     md = [
-        "# HBM traffic of pss_row_kernel, headline workload (256 x 102,400 fp32)",
+        "# HBM traffic of %s, headline workload (256 x 102,400 fp32)" % kname,
         "",
         "Commands (from the repository root on the MI355X box; then, on any host,",
         "`python3 bench.py --traffic-from <fetch dir> <write dir>` wrote this file):",
@@ -376,7 +377,7 @@ def traffic_from_pmc(fetch_dir, write_dir, out_path):
         "",
         "| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes per launch (scaled) |",
         "|---|---|---|---|",
-        "| pss_row_kernel | %.1f | %.1f | %.0f |" % (fc["row_kib"], wc["row_kib"], row),
+        "| %s | %.1f | %.1f | %.0f |" % (kname, fc["row_kib"], wc["row_kib"], row),
         "",
         "Algorithmic bytes per launch: 256 x (102,400 x 4 + 4 x 64 + 44) = %d." % (256 * (409600 + 256 + 44)),
         "",
@@ -406,6 +407,7 @@ def main():
     ap.add_argument("--lmhead-steps", type=int, default=50)
     ap.add_argument("--general", action="store_true", help="force the general kernel")
     ap.add_argument("--split", action="store_true", help="force the two-kernel form")
+    ap.add_argument("--fused", action="store_true", help="force the LDS-staged fused form")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run device-to-device copies of one headline batch (traffic calibration)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -436,8 +438,10 @@ def main():
         lat = bench_latency(args.latency_steps)
         print(json.dumps({"latency_b1": lat}), flush=True)
         return
-    flags = S.ENQ_GENERAL if args.general else (S.ENQ_SPLIT if args.split else 0)
-    kernel = "general" if args.general else ("split" if args.split else "fused")
+    flags = (S.ENQ_GENERAL if args.general else S.ENQ_SPLIT if args.split else
+             S.ENQ_FUSED if args.fused else 0)
+    kernel = ("general" if args.general else "split" if args.split else "fused" if args.fused
+              else "resident")
     log("generating headline workload")
     head = WL.headline(seed=0)
     log("headline: 256 x 102400 fp32")
@@ -476,10 +480,11 @@ def main():
         with open(tpath) as f:
             txt = f.read()
         if "```json" in txt:
-            traffic = json.loads(txt.split("```json", 1)[1].split("```", 1)[0]).get(
-                "row_kernel_hbm_bytes_per_launch")
-        if kernel != "fused":
-            traffic = None
+            tj = json.loads(txt.split("```json", 1)[1].split("```", 1)[0])
+            # counters read for the kernel form this run times, else none
+            kname = {"resident": "pss_res_kernel", "fused": "pss_row_kernel"}.get(kernel)
+            if tj.get("kernel") == kname:
+                traffic = tj.get("row_kernel_hbm_bytes_per_launch")
     # dominant (fused: only) kernel: algorithmic bytes per launch / mean
     # per-launch time from HIP events on the sampler's stream bracketing the
     # timed back-to-back launches (events around single launches, which add

@@ -130,6 +130,11 @@ typedef struct {
  * later group is skipped: a caller can queue group n + 1 before it has read
  * group n's tokens and still end in the state of the unpipelined loop. */
 #define PSS_ENQ_GATED 16u
+/* Force the register-resident form (one workgroup per row holding the whole
+ * row in registers; rows of 16-byte aligned fp32 up to 102,400 ids or fp16 up
+ * to 106,496 ids, the fused form otherwise).  The automatic choice takes it
+ * for batches above the small-batch form's range.  Identical results. */
+#define PSS_ENQ_RESIDENT 32u
 
 /* Words per row of kept_mask. */
 uint32_t pss_mask_words(uint32_t vocab);

@@ -15,6 +15,7 @@
 #include "pss_general.h"
 #include "pss_score.h"
 #include "pss_stream.h"
+#include "pss_resident.h"
 #include "pss_sampler_priv.h"
 #include "pumice_sampler.h"
 
@@ -303,11 +304,12 @@ extern "C" pss_status pss_enqueue_ex(pss_sampler* s, const void* logits, uint32_
         }
         const hipEvent_t split = opts ? (hipEvent_t)opts->split_event : NULL;
         const uint32_t fl = opts ? opts->flags : 0u;
-        const int form = (fl & PSS_ENQ_SPLIT)   ? PSS_FORM_SPLIT
-                         : (fl & PSS_ENQ_FUSED) ? PSS_FORM_FUSED
-                         : (fl & PSS_ENQ_SMALL) ? PSS_FORM_SMALL
-                                                : -1;
-        if (pss_stream_launch(a, rows, max_k, max_w, form, s->stream, split) != hipSuccess) return PSS_ERR_HIP;
+        const int form = (fl & PSS_ENQ_SPLIT)      ? PSS_FORM_SPLIT
+                         : (fl & PSS_ENQ_FUSED)    ? PSS_FORM_FUSED
+                         : (fl & PSS_ENQ_SMALL)    ? PSS_FORM_SMALL
+                         : (fl & PSS_ENQ_RESIDENT) ? PSS_FORM_RESIDENT
+                                                   : -1;
+        if (pss_launch_rows(a, rows, max_k, max_w, form, s->stream, split) != hipSuccess) return PSS_ERR_HIP;
         return PSS_OK;
     }
     pss_general_kernel<<<dim3(rows), dim3(PSS_GEN_NT), 0, s->stream>>>(a);

@@ -114,6 +114,12 @@ struct pss_fin_small {
     uint32_t nk;
     uint32_t fail;
     uint64_t gtot; /* finisher gather totals (overflowed, not filtered, entries) */
+    /* two-wave tail: the key-order results wave 0 hands to wave 1 (hflag
+     * is cleared with nk, before the caller's last barrier) */
+    uint32_t hflag;
+    uint32_t htau;
+    uint32_t htmax;
+    uint64_t hzk;
 };
 
 struct pss_fin_shared {
@@ -435,68 +441,127 @@ __device__ __forceinline__ void pss_wave_tail4(const pss_args& a, uint32_t row, 
     }
 }
 
+/* Ascending sort of one u32 per lane across the wave (bitonic, DPP /
+ * permlane exchanges); `lane` is the lane index, computed once by the caller
+ * so the per-stage directions are not recomputed. */
+template <int KB, int J>
+__device__ __forceinline__ uint32_t pss_sort_stage(uint32_t x, uint32_t lane) {
+    uint32_t y;
+    if constexpr (J <= 8) {
+        y = lane_xor<J>(x);
+    } else if constexpr (J == 16) {
+        const auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        y = (lane & 16u) ? p[0] : p[1];
+    } else {
+        const auto p = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        y = (lane & 32u) ? p[0] : p[1];
+    }
+    const bool lowSide = (lane & (uint32_t)J) == 0u;
+    const bool asc = KB == 64 ? true : (lane & (uint32_t)KB) == 0u;
+    return lowSide == asc ? min(x, y) : max(x, y);
+}
+__device__ __forceinline__ uint32_t pss_sort64_asc(uint32_t x, uint32_t lane) {
+    x = pss_sort_stage<2, 1>(x, lane);
+    x = pss_sort_stage<4, 2>(x, lane);
+    x = pss_sort_stage<4, 1>(x, lane);
+    x = pss_sort_stage<8, 4>(x, lane);
+    x = pss_sort_stage<8, 2>(x, lane);
+    x = pss_sort_stage<8, 1>(x, lane);
+    x = pss_sort_stage<16, 8>(x, lane);
+    x = pss_sort_stage<16, 4>(x, lane);
+    x = pss_sort_stage<16, 2>(x, lane);
+    x = pss_sort_stage<16, 1>(x, lane);
+    x = pss_sort_stage<32, 16>(x, lane);
+    x = pss_sort_stage<32, 8>(x, lane);
+    x = pss_sort_stage<32, 4>(x, lane);
+    x = pss_sort_stage<32, 2>(x, lane);
+    x = pss_sort_stage<32, 1>(x, lane);
+    x = pss_sort_stage<64, 32>(x, lane);
+    x = pss_sort_stage<64, 16>(x, lane);
+    x = pss_sort_stage<64, 8>(x, lane);
+    x = pss_sort_stage<64, 4>(x, lane);
+    x = pss_sort_stage<64, 2>(x, lane);
+    return pss_sort_stage<64, 1>(x, lane);
+}
+
 /*
  * Finisher tail for 1..64 entries (src) that hold every element at or above
- * the K-th largest, run by wave 0, one entry per lane: a 32-bit DPP/permlane
- * sort of the keys in descending order gives the K-th largest (position
- * K - 1, when `find_k`; otherwise tauK is exact already) and the key-order
- * mass scan for the top-p cut (every quantity depends on the key alone, so
- * ties need no order); min-p and the masses on each lane's own entry; a
- * 32-bit sort of (id << 6) | lane orders the kept ids, their masses come from
- * the owning lanes (ds_bpermute), and the first id whose cumulative mass
- * exceeds the draw target is the token.
+ * the K-th largest, run by waves 0 and 1 together (threads 0..127), one entry
+ * per lane in each.  The key order and the id order are independent, so the
+ * two sorts run on two SIMDs at once:
+ *   wave 0: the keys in descending order give the K-th largest (position
+ *     K - 1, when `find_k`; otherwise tauK is exact already) and the
+ *     key-order mass scan for the top-p cut (every quantity depends on the
+ *     key alone, so ties need no order); it hands the cut tau (with the row
+ *     maximum and Z_k) to wave 1 through sh and ends;
+ *   wave 1: (id << 6) | lane sorted in ascending order, each entry's key by
+ *     ds_bpermute, its mass; once tau arrives, min-p and the cut on each
+ *     entry, the kept mass in ascending-id order, the first id whose
+ *     cumulative mass exceeds the draw target, the verification outputs and
+ *     the epilogue.
+ * sh.hflag must be zero on entry (cleared before the caller's last barrier).
  */
-__device__ __forceinline__ void pss_wave_tail64(const pss_args& a, uint32_t row, const pss_rowcfg& c,
-                                                const unsigned long long* src, uint32_t cnt, uint32_t tauK,
-                                                bool find_k, const pss_row_pre& pre, uint32_t u24,
-                                                uint32_t newRng) {
-    const uint32_t lane = pss_tid() & 63u;
+__device__ __forceinline__ void pss_tail64_2w(const pss_args& a, uint32_t row, const pss_rowcfg& c,
+                                              const unsigned long long* src, uint32_t cnt, uint32_t tauK,
+                                              bool find_k, const pss_row_pre& pre, uint32_t u24, uint32_t newRng,
+                                              pss_fin_small& sh) {
+    const uint32_t lane = threadIdx.x & 63u;
     const bool valid = lane < cnt;
     const uint64_t my = valid ? src[lane] : 0ull;
     const uint32_t mkey = (uint32_t)(my >> 32), mid = (uint32_t)my;
-    /* S5/S6 over the keys in descending order (keys of entries are at
-     * least key(-inf) > 0; missing lanes sort last as key 0).  Every
-     * quantity here depends on the key alone, so ties need no order. */
-    const uint32_t skey = ~dpp_sort_asc_u32(valid ? ~mkey : 0xFFFFFFFFu);
-    const uint32_t tmaxKey = wave_read_u32(skey, 0u);
-    if (find_k) tauK = wave_read_u32(skey, (c.K <= cnt ? c.K : cnt) - 1u);
-    const bool sv = valid && skey >= tauK;
-    const float tmax = pss_unkey(tmaxKey);
-    const uint64_t sq = sv ? pss_fixq(pss_prob(pss_unkey(skey), tmax)) : 0ull;
-    const uint64_t P = wave_incl_scan_u64(sq);
-    const uint64_t zk = wave_read_u64(P, 63);
-    uint32_t tau = tauK;
-    if (c.useTopP) {
-        const uint64_t need = pss_topp_need(c.topP, zk);
-        const uint64_t m = __ballot(sv && P >= need);
-        const uint32_t tauP = wave_read_u32(skey, (uint32_t)__ffsll((long long)m) - 1u);
-        tau = tauP > tau ? tauP : tau;
+    if (threadIdx.x < 64u) {
+        /* S5/S6 over the keys in descending order (keys of entries are at
+         * least key(-inf) > 0; missing lanes sort last as key 0) */
+        const uint32_t skey = ~pss_sort64_asc(valid ? ~mkey : 0xFFFFFFFFu, lane);
+        const uint32_t tmaxKey = wave_read_u32(skey, 0u);
+        if (find_k) tauK = wave_read_u32(skey, (c.K <= cnt ? c.K : cnt) - 1u);
+        const bool sv = valid && skey >= tauK;
+        const float tmax = pss_unkey(tmaxKey);
+        const uint64_t sq = sv ? pss_fixq(pss_prob(pss_unkey(skey), tmax)) : 0ull;
+        const uint64_t P = wave_incl_scan_u64(sq);
+        const uint64_t zk = wave_read_u64(P, 63);
+        uint32_t tau = tauK;
+        if (c.useTopP) {
+            const uint64_t need = pss_topp_need(c.topP, zk);
+            const uint64_t m = __ballot(sv && P >= need);
+            const uint32_t tauP = wave_read_u32(skey, (uint32_t)__ffsll((long long)m) - 1u);
+            tau = tauP > tau ? tauP : tau;
+        }
+        if (lane == 0u) {
+            sh.htau = tau;
+            sh.htmax = tmaxKey;
+            sh.hzk = zk;
+            __hip_atomic_store(&sh.hflag, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        return;
     }
-    /* S7 on each lane's own entry */
-    const float sp = valid ? pss_prob(pss_unkey(mkey), tmax) : 0.0f;
-    const bool kp = valid && mkey >= tau && (!c.useMinP || sp >= c.minP);
-    const uint64_t kq = kp ? pss_fixq(sp) : 0ull;
-    const uint64_t Z = wave_sum_u64(kq);
-    const uint32_t keptCount = (uint32_t)__popcll(__ballot(kp));
-    const uint32_t lastAll = wave_max_u32(kp ? mid + 1u : 0u);
-    const uint32_t sid = mid;
-
-    /* S8: kept entries in id order ((id << 6) | lane: ids < 2^18), their
-     * masses fetched from the owning lanes, cumulative mass, first
-     * crossing */
-    const uint64_t target = pss_draw_target(u24, Z);
-    const uint32_t ix = dpp_sort_asc_u32(kp ? ((mid << 6) | lane) : 0xFFFFFFFFu);
+    /* wave 1: the entries in id order ((id << 6) | lane: ids < 2^18) with
+     * their keys and masses, while wave 0 finds the cut */
+    const uint32_t tmaxKey = __builtin_amdgcn_readfirstlane(wave_max_u32(valid ? mkey : 0u));
+    const uint32_t ix = pss_sort64_asc(valid ? ((mid << 6) | lane) : 0xFFFFFFFFu, lane);
     const bool iv = ix != 0xFFFFFFFFu;
-    const int from = (int)((ix & 63u) << 2);
-    const uint32_t qlo = (uint32_t)__builtin_amdgcn_ds_bpermute(from, (int)(uint32_t)kq);
-    const uint32_t qhi = (uint32_t)__builtin_amdgcn_ds_bpermute(from, (int)(uint32_t)(kq >> 32));
-    const uint64_t C = wave_incl_scan_u64(iv ? (((uint64_t)qhi << 32) | qlo) : 0ull);
-    const uint64_t hit = __ballot(iv && C > target);
+    const uint32_t ik = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((ix & 63u) << 2), (int)mkey);
+    const float tmax = pss_unkey(tmaxKey);
+    const float ip = iv ? pss_prob(pss_unkey(ik), tmax) : 0.0f;
+    const uint64_t iq = pss_fixq(ip);
+    while (__hip_atomic_load(&sh.hflag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0u)
+        __builtin_amdgcn_s_sleep(1);
+    const uint32_t tau = sh.htau;
+    /* S7 on each entry, S8: the kept mass in ascending-id order, the first
+     * crossing of the target */
+    const bool kp = iv && ik >= tau && (!c.useMinP || ip >= c.minP);
+    const uint64_t C = wave_incl_scan_u64(kp ? iq : 0ull);
+    const uint64_t Z = wave_read_u64(C, 63);
+    const uint64_t km = __ballot(kp);
+    const uint32_t keptCount = (uint32_t)__popcll(km);
+    const uint64_t target = pss_draw_target(u24, Z);
+    const uint64_t hit = __ballot(kp && C > target);
     uint32_t tok, flags = 0;
     if (hit) {
         tok = wave_read_u32(ix, (uint32_t)__ffsll((long long)hit) - 1u) >> 6;
     } else {
-        tok = lastAll > 0u ? lastAll - 1u : 0u;
+        /* the largest kept id (the last kept entry in id order) */
+        tok = km ? wave_read_u32(ix, 63u - (uint32_t)__builtin_clzll(km)) >> 6 : 0u;
         flags |= PSS_INFO_FALLBACK;
     }
 
@@ -508,8 +573,9 @@ __device__ __forceinline__ void pss_wave_tail64(const pss_args& a, uint32_t row,
             for (uint32_t j = lane; j < a.V; j += 64u) a.probs[(size_t)row * a.probs_stride + j] = 0.0f;
         pss_wait_mem();
         if (kp) {
+            const uint32_t sid = ix >> 6;
             if (a.kept_mask) atomicOr(&a.kept_mask[(size_t)row * a.mask_words + (sid >> 5)], 1u << (sid & 31u));
-            if (a.probs) a.probs[(size_t)row * a.probs_stride + sid] = sp / ((float)Z * 0x1.0p-45f);
+            if (a.probs) a.probs[(size_t)row * a.probs_stride + sid] = ip / ((float)Z * 0x1.0p-45f);
         }
     }
     if (lane == 0) {
@@ -519,7 +585,7 @@ __device__ __forceinline__ void pss_wave_tail64(const pss_args& a, uint32_t row,
         inf.tau_key = tau;
         inf.tmax_key = tmaxKey;
         inf.z_kept = Z;
-        inf.z_topk = zk;
+        inf.z_topk = sh.hzk;
         inf.target = target;
         inf.u24 = u24;
         inf.flags = flags;
@@ -571,6 +637,7 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
         if (tid == 0) {
             sh.nc = 0u;
             sh.nk = 0u;
+            sh.hflag = 0u;
         }
         __syncthreads();
         /* 1. compact */
@@ -697,7 +764,7 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
         }
     }
     if (cnt == 0u) return false;
-    if (tid < 64) pss_wave_tail64(a, row, c, src, cnt, tauK, nc <= 64u || coarse, pre, u24, newRng);
+    if (tid < 128) pss_tail64_2w(a, row, c, src, cnt, tauK, nc <= 64u || coarse, pre, u24, newRng, sh);
     return true;
 }
 
@@ -1465,7 +1532,10 @@ __device__ __forceinline__ void pss_fin_row(const pss_args& a, const sample_para
          * written: sums of at most 256 items stay within their fields */
         const uint64_t mine = over ? (1ull << 54) : (((uint64_t)extra << 32) | (uint64_t)(__popc(keep) + extra));
         uint64_t off64 = 0u, tot64 = 0u;
-        if (tid == 0) sh.f.nk = 0u;
+        if (tid == 0) {
+            sh.f.nk = 0u;
+            sh.f.hflag = 0u;
+        }
         if (NS <= (uint32_t)PSS_WAVE) {
             /* every item in wave 0: a wave scan, no barrier */
             if (tid < PSS_WAVE) {
@@ -1623,7 +1693,7 @@ static inline hipError_t pss_seg_launch(const pss_args& a, uint32_t NS, uint32_t
 /* Streaming forms: fused (one workgroup per row), small-batch (each row over
  * ceil(NS / PSS_SEG_NW) workgroups of one round, finished by the last to
  * arrive), split (two kernels). */
-enum { PSS_FORM_FUSED = 0, PSS_FORM_SMALL = 1, PSS_FORM_SPLIT = 2 };
+enum { PSS_FORM_FUSED = 0, PSS_FORM_SMALL = 1, PSS_FORM_SPLIT = 2, PSS_FORM_RESIDENT = 3 };
 
 static inline uint32_t pss_small_gw(uint32_t NS) { return (NS + PSS_SEG_NW - 1u) / PSS_SEG_NW; }
 

@@ -32,6 +32,7 @@ ENQ_SPLIT = 2
 ENQ_FUSED = 4
 ENQ_SMALL = 8
 ENQ_GATED = 16
+ENQ_RESIDENT = 32
 
 STATUS = {0: "ok", 1: "invalid argument", 2: "allocation failed", 3: "HIP runtime error",
           4: "unsupported", 5: "no gfx950 device"}

@@ -147,8 +147,8 @@ def test_pipelined_matches_unpipelined_state(where, rows):
         assert np.array_equal(a[4][k], b[4][k]), k
 
 
-@pytest.mark.parametrize("flags", [0, S.ENQ_FUSED, S.ENQ_SMALL, S.ENQ_SPLIT, S.ENQ_GENERAL],
-                         ids=["auto", "fused", "small", "split", "general"])
+@pytest.mark.parametrize("flags", [0, S.ENQ_FUSED, S.ENQ_SMALL, S.ENQ_SPLIT, S.ENQ_GENERAL, S.ENQ_RESIDENT],
+                         ids=["auto", "fused", "small", "split", "general", "resident"])
 def test_closed_gate_changes_nothing(flags):
     xs, params, hist = _inputs(24)
     rows = 2

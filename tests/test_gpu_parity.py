@@ -14,8 +14,8 @@ from pumice_amd import workloads as WL
 
 pytestmark = pytest.mark.gpu
 
-PATHS = [0, S.ENQ_FUSED, S.ENQ_SMALL, S.ENQ_SPLIT, S.ENQ_GENERAL]  # auto form, fused, small-batch, two-kernel, general
-PATH_IDS = ["auto", "fused", "small", "split", "general"]
+PATHS = [0, S.ENQ_FUSED, S.ENQ_SMALL, S.ENQ_SPLIT, S.ENQ_GENERAL, S.ENQ_RESIDENT]  # auto form, fused, small-batch, two-kernel, general, resident
+PATH_IDS = ["auto", "fused", "small", "split", "general", "resident"]
 PROB_RTOL = 1e-6                    # normalized probabilities vs fp64
 
 
@@ -104,7 +104,7 @@ WIDE_CASES = {
 }
 
 
-@pytest.mark.parametrize("flags", [0, S.ENQ_FUSED], ids=["auto", "fused"])
+@pytest.mark.parametrize("flags", [0, S.ENQ_FUSED, S.ENQ_RESIDENT], ids=["auto", "fused", "resident"])
 @pytest.mark.parametrize("case", sorted(WIDE_CASES))
 def test_wide_fused(case, flags):
     """The wide fused form (top-k up to 1,024, windows up to 1,024 in LDS):
