@@ -251,6 +251,45 @@ def test_special_values(flags):
                  want_probs=(mode == S.MODE_SAMPLE), where=f"special mode {mode}")
 
 
+def _ulp_run(base, n, rng):
+    """n binary32 values base, base + 1 ulp, ... in random order."""
+    b = np.array([base], np.float32).view(np.uint32)[0]
+    step = np.uint32(1) if base > 0 else np.uint32(0xFFFFFFFF)  # toward +inf
+    v = (b + step * np.arange(n, dtype=np.uint32)).astype(np.uint32).view(np.float32)
+    return rng.permutation(v)
+
+
+@pytest.mark.parametrize("flags", PATHS, ids=PATH_IDS)
+def test_rounding_ties(flags):
+    """Rows whose K-th largest sits where t = l * (1/T) rounds distinct
+    logits to one value (kernels that bound the K-th largest on l must
+    still keep every tied t), where t overflows to +inf, and where t is
+    subnormal; full-width rows so every kernel form takes them."""
+    V = 102400
+    rng = np.random.default_rng(21)
+    rows = 6
+    x = rng.standard_normal((rows, V)).astype(np.float32)
+    T = [3.0, 7.0, 0.1, 1e-30, 1e38, 1.0 / 3.0]
+    x[0, rng.choice(V, 300, replace=False)] = _ulp_run(np.float32(7.0), 300, rng)
+    x[1, rng.choice(V, 300, replace=False)] = _ulp_run(np.float32(-0.03), 300, rng)
+    x[1] -= np.float32(5.0)
+    x[1, rng.choice(V, 300, replace=False)] = _ulp_run(np.float32(-0.03), 300, rng)
+    x[2, rng.choice(V, 300, replace=False)] = _ulp_run(np.float32(7.0), 300, rng)
+    x[3, rng.choice(V, 60, replace=False)] = np.float32(1e9) * (1 + rng.random(60, np.float32))
+    x[4] *= np.float32(1e-3)
+    x[5, rng.choice(V, 300, replace=False)] = _ulp_run(np.float32(1.5), 300, rng)
+    p = S.make_params(rows, temperature=1.0, topK=40, topP=0.97, minP=0.0)
+    p["temperature"] = np.array(T, np.float32)
+    p[1]["topK"] = 150
+    p[5]["topK"] = 200
+    run_both(x, p, np.arange(rows, dtype=np.uint32) + 5, flags=flags, want_probs=True, where="rounding ties")
+    xh = (rng.standard_normal((3, V)) * 4).astype(np.float16)
+    xh[0, rng.choice(V, 100, replace=False)] = np.float16(60000.0)
+    ph = S.make_params(3, temperature=1.0, topK=40, topP=0.97)
+    ph["temperature"] = np.array([1e-35, 1e38, 0.37], np.float32)
+    run_both(xh, ph, np.arange(3, dtype=np.uint32) + 9, flags=flags, where="rounding ties fp16")
+
+
 @pytest.mark.parametrize("flags", PATHS, ids=PATH_IDS)
 def test_fp16_special(flags):
     V = 2048
