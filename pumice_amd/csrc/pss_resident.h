@@ -44,9 +44,6 @@
 #ifndef PSS_RES_DEPTH
 #define PSS_RES_DEPTH 4
 #endif
-#ifndef PSS_RES_PUB
-#define PSS_RES_PUB (-3) /* publish after load NL - 4 */
-#endif
 
 template <int NL, int DT>
 struct pss_res_geom {
@@ -55,13 +52,7 @@ struct pss_res_geom {
     static constexpr uint32_t WSPAN = (uint32_t)NL * LSPAN;   /* ids per wave */
     static constexpr uint32_t VMAX = PSS_RES_NW * WSPAN;
     static constexpr uint32_t BW = (VMAX + 31u) / 32u;        /* window bitmap words */
-    static constexpr int JC = (7 * NL) / 10;                  /* loads 0..JC in registers */
-    static constexpr int NS = NL - JC - 1;                    /* loads JC+1..NL-1 in the LDS stash */
-    /* the waves publish their lane maxima after load P, while the last
-     * loads are still arriving (the bound is then off the critical path) */
-    static constexpr int P0 = PSS_RES_PUB < 0 ? NL - 1 + PSS_RES_PUB : PSS_RES_PUB;
-    static constexpr int P = P0 < JC ? JC : P0;
-    static_assert(P >= JC && P < NL, "publish point among the ring loads");
+    static constexpr int JC = (3 * NL) / 4;                   /* loads 0..JC before the bound */
     /* loads a wave keeps in flight: a CU can have about 50 outstanding, so
      * more would stall the wave at its next request, ahead of the work on
      * the data that has arrived */
@@ -76,54 +67,24 @@ struct pss_res_shared {
     uint32_t wid[PSS_RES_NW][2u * PSS_WAVE];           /* per wave: the distinct window ids in its range */
     uint32_t pub[PSS_RES_NW * 16u];                    /* per wave: its lanes' largest maxima, sorted */
     unsigned long long best[PSS_RES_NW];               /* greedy rows: each wave's (key << 32) | ~id */
-    uint4 stash[PSS_RES_NW][pss_res_geom<NL, DT>::NS][PSS_WAVE]; /* loads after JC, as loaded */
+    uint32_t wl[PSS_RES_NW];                           /* bit j: load j of the wave holds window ids */
     uint32_t ncl;                                      /* candidates claimed (may exceed PSS_FAST_N) */
-    uint32_t npub;                                     /* waves that have published their maxima */
-    uint32_t ndone;                                    /* waves whose loads have all arrived */
-    uint32_t gflag;                                    /* G and L are set */
-    uint32_t G;                                        /* the list bound (a key of t) */
-    uint32_t L;                                        /* the smallest l reaching it (a key of l) */
+    uint32_t G;                                        /* the bound */
     uint32_t over;                                     /* a wave's range holds more window ids than it keeps */
 };
 
-/* Value e of a load as a float (the raw logit l: fp32 in place, fp16
- * widened). */
+/* Value e of a load as a transformed float: fp32 loads hold t in place; fp16
+ * loads hold the raw halves (excluded elements set to -inf). */
 template <int DT>
-__device__ __forceinline__ float pss_res_l(const uint4& r, int e) {
+__device__ __forceinline__ float pss_res_t(const uint4& r, int e, float invT) {
     const uint32_t w[4] = {r.x, r.y, r.z, r.w};
     if (DT == PSS_DTYPE_F16) {
         const uint16_t h = (uint16_t)(w[e >> 1] >> ((e & 1) * 16));
         _Float16 hf;
         __builtin_memcpy(&hf, &h, 2);
-        return (float)hf;
+        return (float)hf * invT;
     }
     return __uint_as_float(w[e]);
-}
-
-/* max(a, b, c) in one instruction, operands as they are (no NaN
- * canonicalization: a signalling NaN may come out as a quiet NaN, which only
- * loosens the bound built from these maxima, never invalidates it) */
-__device__ __forceinline__ float pss_max3_raw(float a, float b, float c) {
-    float r;
-    __asm__("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
-}
-__device__ __forceinline__ uint32_t pss_pk_max_f16(uint32_t a, uint32_t b) {
-    uint32_t r;
-    __asm__("v_pk_max_f16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-    return r;
-}
-
-/* The largest value of a load (same NaN caveat). */
-template <int DT>
-__device__ __forceinline__ float pss_res_lmax(const uint4& r) {
-    if (DT == PSS_DTYPE_F16) {
-        const uint32_t h = pss_pk_max_f16(pss_pk_max_f16(r.x, r.y), pss_pk_max_f16(r.z, r.w));
-        const uint4 q = make_uint4(h, 0u, 0u, 0u);
-        return pss_max3_raw(pss_res_l<DT>(q, 0), pss_res_l<DT>(q, 1), pss_res_l<DT>(q, 1));
-    }
-    return pss_max3_raw(pss_max3_raw(__uint_as_float(r.x), __uint_as_float(r.y), __uint_as_float(r.z)),
-                        __uint_as_float(r.w), __uint_as_float(r.w));
 }
 
 /* Element e of a load set to -inf (an excluded id). */
@@ -213,14 +174,11 @@ __global__ void __launch_bounds__(PSS_RES_NT) pss_res_kernel(pss_args a, const s
     const uint32_t V = a.V;
     const float NEG_INF = pss_u2f(0xFF800000u);
 
-    /* shared counters, first used after the barrier that ends section 2 */
+    /* shared counters, first used after the bound's barrier */
     if (tid < 256u) f.hist[0][tid] = f.hist[1][tid] = 0u;
     if (tid == 0u) {
         S.ncl = 0u;
         S.over = 0u;
-        S.npub = 0u;
-        S.ndone = 0u;
-        S.gflag = 0u;
         f.nk = 0u;
         f.hflag = 0u;
     }
@@ -285,37 +243,24 @@ __global__ void __launch_bounds__(PSS_RES_NT) pss_res_kernel(pss_args a, const s
         wraw0 = __builtin_amdgcn_raw_buffer_load_b32(rrs, (int)((i0 * esz) & ~3u), 0, 0);
         wraw1 = __builtin_amdgcn_raw_buffer_load_b32(rrs, (int)((i1 * esz) & ~3u), 0, 0);
     }
-    /* the one barrier before the end: the counters are set and every
-     * wave's window marks are in (the row's first loads are in flight) */
-    __syncthreads();
 
-    /* 3. the loads in arrival order.  The bound is built on the raw logits
-     * l: t = l * (1/T) rounded is non-decreasing in l for a finite 1/T > 0,
-     * and canonicalization keeps the order (NaN is the lowest), so the K
-     * largest l are the K largest t; only the elements extracted for the
-     * list are transformed. */
-    bool fb = !greedy && (!cov || !(invT > 0.0f && invT < pss_u2f(0x7F800000u))); /* general algorithm */
+    /* 3. the loads in arrival order */
     /* maxima each wave publishes: 16 x 8 >= K for K <= 128, 16 x 16 up to 256 */
     const uint32_t npub = c.K <= 128u ? 8u : 16u;
-    /* the lane's largest and second largest l (window ids excluded; NaN
-     * never compares greater, so it never enters) and the position (load *
-     * E + element) of the largest */
-    float m1 = NEG_INF, m2 = NEG_INF, m3 = NEG_INF;
-    uint32_t p1 = 0u, p2 = 0u;
-    uint32_t mxk = 0u;   /* the lane's largest list key */
-    float gm = NEG_INF;  /* greedy: the lane's largest l and its first position */
-    uint32_t gi = 0u;
-    uint32_t G = 0u;     /* the list bound, a key of t */
-    float Lx = NEG_INF;  /* the smallest l with key(t) >= G */
+    float m = NEG_INF, m2 = NEG_INF;
+    uint32_t mpos = 0u;
+    uint64_t best = 0ull;
+    uint32_t G = 0u;
+    float Gf = NEG_INF;
+    bool fb = !greedy && !cov; /* general algorithm */
 
-    /* the elements of a load with l >= Lx in lanes with `sel` into the
-     * candidate list */
-    auto extract = [&](const uint4& r, uint32_t id0, bool sel) {
+    /* the elements of a load at or above G into the candidate list */
+    auto extract = [&](const uint4& r, uint32_t id0) {
         uint64_t mk[E];
         uint32_t tot = 0u;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
-            mk[e] = __ballot(sel && pss_res_l<DT>(r, e) >= Lx);
+            mk[e] = __ballot(pss_res_t<DT>(r, e, invT) >= Gf);
             tot += (uint32_t)__popcll(mk[e]);
         }
         if (tot == 0u) return;
@@ -326,13 +271,18 @@ __global__ void __launch_bounds__(PSS_RES_NT) pss_res_kernel(pss_args a, const s
         for (int e = 0; e < E; ++e) {
             const uint32_t pos =
                 base + __builtin_amdgcn_mbcnt_hi((uint32_t)(mk[e] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk[e], 0u));
-            if ((mk[e] >> lane) & 1ull) {
-                const uint32_t k = pss_key(pss_canon(pss_res_l<DT>(r, e) * invT));
-                mxk = k > mxk ? k : mxk;
-                if (pos < PSS_FAST_N) f.cl[pos] = ((unsigned long long)k << 32) | (id0 + (uint32_t)e);
+            if (((mk[e] >> lane) & 1ull) && pos < PSS_FAST_N) {
+                const float te = pss_res_t<DT>(r, e, invT);
+                f.cl[pos] = ((unsigned long long)pss_key(pss_canon(te)) << 32) | (id0 + (uint32_t)e);
             }
             base += (uint32_t)__popcll(mk[e]);
         }
+    };
+    auto gmax = [&](const uint4& r) -> float {
+        float g = pss_res_t<DT>(r, 0, invT);
+#pragma unroll
+        for (int e = 1; e < E; ++e) g = fmaxf(g, pss_res_t<DT>(r, e, invT));
+        return g;
     };
     /* ids at or beyond V (the buffer returned 0 for them) become -inf */
     auto clip = [&](uint4& r, uint32_t j) {
@@ -343,17 +293,25 @@ __global__ void __launch_bounds__(PSS_RES_NT) pss_res_kernel(pss_args a, const s
                 if (id0 + (uint32_t)e >= V) pss_res_kill<DT>(r, e);
         }
     };
-    /* greedy: the lane's largest l, the first on ties (a lane's positions
-     * run in id order; NaN never compares greater) */
     auto greedy_upd = [&](uint4& r, uint32_t j) {
         clip(r, j);
+        const uint32_t id0 = idw + j * Gm::LSPAN + lane * (uint32_t)E;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
-            const float x = pss_res_l<DT>(r, e);
-            const bool gt = x > gm;
-            gm = gt ? x : gm;
-            gi = gt ? j * (uint32_t)E + (uint32_t)e : gi;
+            const uint64_t b = ((uint64_t)pss_key(pss_canon(pss_res_t<DT>(r, e, 1.0f))) << 32) |
+                               (uint64_t)(0xFFFFFFFFu - (id0 + (uint32_t)e));
+            best = b > best ? b : best;
         }
+    };
+    /* t = l * (1/T) in place (fp32; fp16 values are widened where used) */
+    auto transform = [&](uint4& r, uint32_t j) {
+        if (DT == PSS_DTYPE_F32) {
+            r.x = __float_as_uint(__uint_as_float(r.x) * invT);
+            r.y = __float_as_uint(__uint_as_float(r.y) * invT);
+            r.z = __float_as_uint(__uint_as_float(r.z) * invT);
+            r.w = __float_as_uint(__uint_as_float(r.w) * invT);
+        }
+        clip(r, j);
     };
     /* window ids of load j: out of the bound and the list */
     auto exclude = [&](uint4& r, uint32_t j) {
@@ -365,81 +323,39 @@ __global__ void __launch_bounds__(PSS_RES_NT) pss_res_kernel(pss_args a, const s
                 if ((wb >> e) & 1u) pss_res_kill<DT>(r, e);
         }
     };
-    /* sampled rows: clip, exclude, track */
-    auto take = [&](uint4& r, uint32_t j) {
-        clip(r, j);
-        exclude(r, j);
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const float x = pss_res_l<DT>(r, e);
-            const uint32_t pos = j * (uint32_t)E + (uint32_t)e;
-            const bool g1 = x > m1, g2 = x > m2, g3 = x > m3;
-            m3 = g2 ? m2 : (g3 ? x : m3);
-            m2 = g1 ? m1 : (g2 ? x : m2);
-            p2 = g1 ? p1 : (g2 ? pos : p2);
-            m1 = g1 ? x : m1;
-            p1 = g1 ? pos : p1;
-        }
-    };
-
-    /* each wave publishes its largest lane maxima (sorted, over loads
-     * 0..P) and counts itself; every published value is a distinct
-     * element's */
-    auto publish = [&]() {
-        const uint32_t sk = ~dpp_sort_asc_u32(~pss_key(pss_canon(m1))); /* descending */
-        if (lane < npub) S.pub[wave * npub + lane] = sk;
-        if (lane == 0u) __hip_atomic_fetch_add(&S.npub, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-    };
 
     /* 3a. loads 0..JC on arrival (the next load requested before each
-     * wait), kept in registers */
+     * wait): transformed, window ids excluded, the lane's running maximum */
 #pragma unroll
     for (int j = 0; j <= Gm::JC; ++j) {
         if (j + Gm::D < NL) issue1(j + Gm::D);
-        if (greedy)
+        if (greedy) {
             greedy_upd(raw[j], (uint32_t)j);
-        else if (!fb)
-            take(raw[j], (uint32_t)j);
-    }
-    if (!greedy && S.over) fb = true; /* too many window ids */
-    if (Gm::P == Gm::JC && !greedy && !fb) publish();
-    /* 3b. loads JC+1..NL-1 through the ring: load j in slot (j - JC - 1) %
-     * RS, load j + D requested into the slot freed by load j - 1; sampled
-     * rows park each in the LDS stash */
-#pragma unroll 1
-    for (uint32_t base = Gm::JC + 1; base < (uint32_t)NL; base += RS) {
+        } else if (!fb) {
+            transform(raw[j], (uint32_t)j);
+            exclude(raw[j], (uint32_t)j);
+            /* the lane's largest (m, at position mpos) and second largest
+             * (m2) values; NaN never enters either */
 #pragma unroll
-        for (int s = 0; s < RS; ++s) {
-            const uint32_t j = base + (uint32_t)s;
-            if (j + Gm::D < (uint32_t)NL) ring[(s + Gm::D) % RS] = ld(j + Gm::D);
-            if (j < (uint32_t)NL) {
-                uint4& r = ring[s];
-                if (greedy) {
-                    greedy_upd(r, j);
-                } else if (!fb) {
-                    take(r, j);
-                    S.stash[wave][j - (uint32_t)Gm::JC - 1u][lane] = r;
-                    if (Gm::P > Gm::JC && j == (uint32_t)Gm::P) publish();
-                }
+            for (int e = 0; e < E; ++e) {
+                const float x = pss_res_t<DT>(raw[j], e, invT);
+                m2 = fminf(fmaxf(m2, x), m);
+                mpos = x > m ? (uint32_t)(j * E + e) : mpos;
+                m = fmaxf(m, x);
             }
         }
     }
-    /* 3c. the bound.  The first wave with all its loads waits for every
-     * wave's maxima and computes it while the others finish loading: the
-     * K-th largest of the published maxima (resolved to 24 bits: a lower
-     * bound of it, K distinct elements at or above it) is a key g of l; G =
-     * key(t) of it and L = the smallest l whose t reaches G.  Then each wave
-     * puts its elements with l >= L and its penalized window values at or
-     * above G into the list: a lane whose second largest is below L has at
-     * most one such element, its largest, at a known position; only lanes
-     * with two or more scan their loads. */
+    /* 3b. the bound: window marks complete, exclusions, lane maxima, each
+     * wave's largest published, one barrier, the K-th largest of them all
+     * (resolved to 24 bits: a lower bound of it); then the candidates of
+     * loads 0..JC and the penalized window values */
     if (!greedy && !fb) {
-        uint32_t first = 0u;
-        if (lane == 0u) first = __hip_atomic_fetch_add(&S.ndone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        first = __builtin_amdgcn_readfirstlane(first);
-        if (first == 0u) {
-            while (__hip_atomic_load(&S.npub, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < PSS_RES_NW)
-                __builtin_amdgcn_s_sleep(1);
+        const uint32_t sk = ~dpp_sort_asc_u32(~pss_key(pss_canon(m))); /* descending */
+        if (lane < npub) S.pub[wave * npub + lane] = sk;
+        __syncthreads();
+        /* one wave searches (the search is scalar work, and the CU's scalar
+         * unit is shared by all its waves) */
+        if (wave == 0u) {
             uint32_t g;
             if (npub == 8u) {
                 const uint32_t v[2] = {S.pub[2u * lane], S.pub[2u * lane + 1u]};
@@ -449,65 +365,33 @@ __global__ void __launch_bounds__(PSS_RES_NT) pss_res_kernel(pss_args a, const s
                                        S.pub[4u * lane + 3u]};
                 g = wave_kth_largest<4, 24>(v, c.K);
             }
-            /* each binary32 t has at most three binary32 preimages l while
-             * both are normal; a longer run (t overflowing to inf, subnormal
-             * t) takes the general path (G = 0) */
-            uint32_t Gt = 0u, lk = g;
-            if (g > PSS_KEY_NEG_INF) {
-                Gt = pss_key(pss_canon(pss_unkey(g) * invT));
-                int it = 0;
-                for (; it < 8 && lk > PSS_KEY_NEG_INF + 1u; ++it)
-                    if (pss_key(pss_canon(pss_unkey(lk - 1u) * invT)) >= Gt) --lk;
-                    else break;
-                if (it == 8 || lk <= PSS_KEY_NEG_INF + 1u || Gt <= PSS_KEY_NEG_INF) Gt = 0u;
-            }
-            if (lane == 0u) {
-                S.G = Gt;
-                S.L = lk;
-                __hip_atomic_store(&S.gflag, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-            }
-        } else {
-            while (__hip_atomic_load(&S.gflag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0u)
-                __builtin_amdgcn_s_sleep(1);
+            if (lane == 0u) S.G = g;
         }
+        __syncthreads();
         G = __builtin_amdgcn_readfirstlane(S.G);
-        Lx = pss_unkey(__builtin_amdgcn_readfirstlane(S.L));
-        if (G <= PSS_KEY_NEG_INF) {
-            fb = true; /* no usable bound (every element could be kept) */
+        Gf = pss_unkey(G);
+        if (G <= PSS_KEY_NEG_INF || S.over) {
+            fb = true; /* no finite bound (every element could be kept), or too many window ids */
         } else {
-            /* a lane with at most two elements at or above L: its largest
-             * and second largest, at known positions */
-            const bool multi = m3 >= Lx;
-            const bool e1 = !multi && m1 >= Lx, e2 = !multi && m2 >= Lx;
-            const uint64_t bm1 = __ballot(e1), bm2 = __ballot(e2);
-            if (bm1) {
-                const uint32_t n1 = (uint32_t)__popcll(bm1);
-                uint32_t b0 = 0u;
-                if (lane == 0u) b0 = atomicAdd(&S.ncl, n1 + (uint32_t)__popcll(bm2));
-                const uint32_t base = __builtin_amdgcn_readfirstlane(b0);
-                auto put = [&](bool on, uint64_t bm, uint32_t at, float x, uint32_t p) {
-                    const uint32_t pos = at + __builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32),
-                                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u));
-                    if (on) {
-                        const uint32_t k = pss_key(pss_canon(x * invT));
-                        const uint32_t id = idw + (p / (uint32_t)E) * Gm::LSPAN + lane * (uint32_t)E + p % (uint32_t)E;
-                        mxk = k > mxk ? k : mxk;
-                        if (pos < PSS_FAST_N) f.cl[pos] = ((unsigned long long)k << 32) | id;
-                    }
-                };
-                put(e1, bm1, base, m1, p1);
-                if (bm2) put(e2, bm2, base + n1, m2, p2);
-            }
-            if (__ballot(multi)) {
+            /* loads 0..JC: a lane whose second largest value is below G has
+             * at most one element at or above it, its largest; only a wave
+             * with a lane holding two or more scans its loads */
+            if (__ballot(m2 >= Gf)) {
 #pragma unroll
                 for (int i = 0; i <= Gm::JC; ++i)
-                    if (__ballot(multi && pss_res_lmax<DT>(raw[i]) >= Lx))
-                        extract(raw[i], idw + (uint32_t)i * Gm::LSPAN + lane * (uint32_t)E, multi);
-#pragma unroll
-                for (int i = 0; i < Gm::NS; ++i) {
-                    const uint4 r = S.stash[wave][i][lane];
-                    if (__ballot(multi && pss_res_lmax<DT>(r) >= Lx))
-                        extract(r, idw + (uint32_t)(Gm::JC + 1 + i) * Gm::LSPAN + lane * (uint32_t)E, multi);
+                    if (__ballot(gmax(raw[i]) >= Gf))
+                        extract(raw[i], idw + (uint32_t)i * Gm::LSPAN + lane * (uint32_t)E);
+            } else {
+                const bool p = m >= Gf;
+                const uint64_t bm = __ballot(p);
+                if (bm) {
+                    uint32_t b0 = 0u;
+                    if (lane == 0u) b0 = atomicAdd(&S.ncl, (uint32_t)__popcll(bm));
+                    const uint32_t pos = __builtin_amdgcn_readfirstlane(b0) +
+                                         __builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32),
+                                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u));
+                    const uint32_t id = idw + (mpos / (uint32_t)E) * Gm::LSPAN + lane * (uint32_t)E + mpos % (uint32_t)E;
+                    if (p && pos < PSS_FAST_N) f.cl[pos] = ((unsigned long long)pss_key(pss_canon(m)) << 32) | id;
                 }
             }
             if (nown) {
@@ -539,7 +423,7 @@ __global__ void __launch_bounds__(PSS_RES_NT) pss_res_kernel(pss_args a, const s
                                              __builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32),
                                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u));
                         if (keep && pos < PSS_FAST_N) f.cl[pos] = ent;
-                        if (keep) mxk = (uint32_t)(ent >> 32) > mxk ? (uint32_t)(ent >> 32) : mxk;
+                        m = fmaxf(m, keep ? pss_unkey((uint32_t)(ent >> 32)) : NEG_INF);
                     }
                 };
                 win(lane, wraw0);
@@ -547,11 +431,31 @@ __global__ void __launch_bounds__(PSS_RES_NT) pss_res_kernel(pss_args a, const s
             }
         }
     }
+    /* 3c. loads JC+1..NL-1 through the ring: load j in slot (j - JC - 1) %
+     * RS, load j + D requested into the slot freed by load j - 1 */
+#pragma unroll 1
+    for (uint32_t base = Gm::JC + 1; base < (uint32_t)NL; base += RS) {
+#pragma unroll
+        for (int s = 0; s < RS; ++s) {
+            const uint32_t j = base + (uint32_t)s;
+            if (j + Gm::D < (uint32_t)NL) ring[(s + Gm::D) % RS] = ld(j + Gm::D);
+            if (j < (uint32_t)NL) {
+                uint4& r = ring[s];
+                if (greedy) {
+                    greedy_upd(r, j);
+                } else if (!fb) {
+                    transform(r, j);
+                    exclude(r, j);
+                    const float g = gmax(r);
+                    m = fmaxf(m, g);
+                    if (__ballot(g >= Gf)) extract(r, idw + j * Gm::LSPAN + lane * (uint32_t)E);
+                }
+            }
+        }
+    }
 
     /* 4. the row finishes from the candidate list */
     if (greedy) {
-        const uint32_t gid = idw + (gi / (uint32_t)E) * Gm::LSPAN + lane * (uint32_t)E + gi % (uint32_t)E;
-        uint64_t best = ((uint64_t)pss_key(pss_canon(gm)) << 32) | (uint64_t)(0xFFFFFFFFu - gid);
         best = wave_max_u64(best);
         if (lane == 0u) S.best[wave] = best;
         __syncthreads();
@@ -561,8 +465,9 @@ __global__ void __launch_bounds__(PSS_RES_NT) pss_res_kernel(pss_args a, const s
         pss_greedy_finish<PSS_RES_NT>(a, row, best);
         return;
     }
-    /* each wave's largest list key, for the finisher's radix path */
-    const uint32_t mkey = wave_max_u32(mxk);
+    /* each wave's largest list value, for the finisher's radix path (the row
+     * maximum is at or above G, so it is in the list) */
+    const uint32_t mkey = wave_max_u32(pss_key(pss_canon(m)));
     if (lane == 0u) f.mx[wave] = mkey;
     __syncthreads();
     const uint32_t n = S.ncl;
