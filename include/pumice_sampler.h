@@ -230,6 +230,31 @@ typedef struct {
 
 pss_status pss_get_state_ptrs(pss_sampler* s, pss_state_ptrs* out);
 
+/* One sampling or greedy step that allocates nothing (no counterpart in the
+ * reference).  For callers that cannot allocate device memory: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * It is pss_enqueue_ex without a sampler object: the caller passes every
+ * input and output as device pointers (params [rows], the state buffers of
+ * `state` laid out as pss_state_ptrs describes for `rows` rows, logits with
+ * `row_stride` elements between rows) and the stream; the workspace of the
+ * small-batch form is a per-GPU array inside the library, set up on the first
+ * call on each device (the device current at the call).
+ *   - rows <= PSS_NOALLOC_MAX_ROWS, else PSS_ERR_INVALID_ARG; modes
+ *     PSS_MODE_GREEDY and PSS_MODE_SAMPLE; opts may carry row_info,
+ *     kept_mask, probs and host_tokens, but no flags or split_event.
+ *   - max_topk / max_window: upper bounds of the rows' topK and
+ *     penaltyLength, used only to choose the kernel form (any values give the
+ *     same results).
+ *   - Calls on one GPU share its workspace: calls that overlap in time on one
+ *     GPU (different streams, no ordering between them) race.
+ * Same results as pss_enqueue_ex on the same inputs. */
+#define PSS_NOALLOC_MAX_ROWS 16u
+pss_status pss_enqueue_noalloc(const sample_params* params, const pss_state_ptrs* state, uint32_t vocab,
+                               const void* logits, uint32_t dtype, uint64_t row_stride, uint32_t rows,
+                               uint32_t mode, uint32_t do_increment, uint32_t pass_idx, uint32_t rng_mode,
+                               uint32_t max_topk, uint32_t max_window, const pss_enqueue_opts* opts,
+                               void* hip_stream);
+
 /* Host-side request sanitization of the reference's stdin server
  * (src/compute.c:113-114): penaltyLength clamped to 1024, seed 0 -> 1. */
 pss_status pss_sanitize_request(sample_params* params, uint32_t* seed);

@@ -12,6 +12,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "pss_general.h"
 #include "pss_score.h"
 #include "pss_stream.h"
@@ -360,4 +362,98 @@ extern "C" pss_status pss_get_state_ptrs(pss_sampler* s, pss_state_ptrs* out) {
     out->step = s->d_step;
     out->history = s->d_hist;
     return PSS_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* the entry point that allocates nothing                                    */
+/* ------------------------------------------------------------------------ */
+
+/* Workspace of the small-batch and two-kernel forms for up to
+ * PSS_NOALLOC_MAX_ROWS rows: per-row bound, arrival ticket and candidate
+ * pool.  One copy per GPU, held until the process ends.  In host code this
+ * name is a host-side stand-in, not a device address: only the pointer from
+ * hipGetSymbolAddress (kept per device below) is ever passed to a kernel. */
+static __device__ __align__(256) unsigned char scratch[PSS_NOALLOC_MAX_ROWS * PSS_WS_ROW_BYTES];
+
+#define PSS_NOALLOC_DEVICES 64
+static void* g_scratch_ptr[PSS_NOALLOC_DEVICES]; /* device address of scratch, per device */
+static std::mutex g_scratch_mu;
+
+/* Set-up on the first call on a device (that device current): check it is a
+ * gfx950, look up its copy of scratch and clear it once on the caller's
+ * stream.  The kernels return every counter they use to zero (the bound and
+ * the arrival ticket are reset by the workgroup that finishes the row), so
+ * later calls find it clear. */
+static pss_status noalloc_scratch(hipStream_t st, void** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return PSS_ERR_NO_DEVICE;
+    if (dev >= PSS_NOALLOC_DEVICES) return PSS_ERR_UNSUPPORTED;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return PSS_ERR_NO_DEVICE;
+        if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return PSS_ERR_NO_DEVICE;
+        void* p = NULL;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return PSS_ERR_HIP;
+        const pss_status f = fill_u32(st, (uint32_t*)p, sizeof(scratch) / 4u, 0u);
+        if (f != PSS_OK) return f;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return PSS_OK;
+}
+
+extern "C" pss_status pss_enqueue_noalloc(const sample_params* params, const pss_state_ptrs* state,
+                                          uint32_t vocab, const void* logits, uint32_t dtype,
+                                          uint64_t row_stride, uint32_t rows, uint32_t mode,
+                                          uint32_t do_increment, uint32_t pass_idx, uint32_t rng_mode,
+                                          uint32_t max_topk, uint32_t max_window,
+                                          const pss_enqueue_opts* opts, void* hip_stream) {
+    if (!params || !state || !logits || !state->result || !state->token_ids || !state->position ||
+        !state->rng || !state->step || !state->history)
+        return PSS_ERR_INVALID_ARG;
+    if (rows == 0 || rows > PSS_NOALLOC_MAX_ROWS || vocab == 0) return PSS_ERR_INVALID_ARG;
+    if (vocab > PSS_MAX_VOCAB) return PSS_ERR_UNSUPPORTED;
+    if (dtype != PSS_DTYPE_F32 && dtype != PSS_DTYPE_F16) return PSS_ERR_INVALID_ARG;
+    if (mode != PSS_MODE_GREEDY && mode != PSS_MODE_SAMPLE) return PSS_ERR_INVALID_ARG;
+    if (rng_mode != PSS_RNG_XORSHIFT32 && rng_mode != PSS_RNG_PHILOX) return PSS_ERR_INVALID_ARG;
+    if (pass_idx >= PSS_RESULT_SLOTS || row_stride < vocab) return PSS_ERR_INVALID_ARG;
+    if (opts && (opts->flags != 0u || opts->split_event)) return PSS_ERR_INVALID_ARG;
+    if (opts && opts->probs && opts->probs_stride < vocab) return PSS_ERR_INVALID_ARG;
+    const hipStream_t st = (hipStream_t)hip_stream;
+    void* ws = NULL;
+    const pss_status ss = noalloc_scratch(st, &ws);
+    if (ss != PSS_OK) return ss;
+
+    pss_args a;
+    memset(&a, 0, sizeof a);
+    a.logits = logits;
+    a.stride = row_stride;
+    a.V = vocab;
+    a.dtype = dtype;
+    a.mode = mode;
+    a.do_inc = do_increment ? 1u : 0u;
+    a.pass_idx = pass_idx;
+    a.rng_mode = rng_mode;
+    a.params = params;
+    a.rng = state->rng;
+    a.step = state->step;
+    a.position = state->position;
+    a.history = state->history;
+    a.result = state->result;
+    a.token_ids = state->token_ids;
+    a.mask_words = pss_mask_words(vocab);
+    a.ws = ws;
+    a.kmax_cov = PSS_SEG_KMAX;
+    a.wmax_cov = PSS_SEG_WMAX;
+    if (opts) {
+        a.info = opts->row_info;
+        a.kept_mask = opts->kept_mask;
+        a.probs = opts->probs;
+        a.probs_stride = opts->probs_stride;
+        a.host_tokens = opts->host_tokens;
+    }
+    /* the automatic form choice; rows <= PSS_NOALLOC_MAX_ROWS, so a form
+     * that uses the workspace stays inside scratch */
+    return pss_launch_rows(a, rows, max_topk, max_window, -1, st, NULL) == hipSuccess ? PSS_OK : PSS_ERR_HIP;
 }

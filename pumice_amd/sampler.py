@@ -70,8 +70,21 @@ EXPORTS = [
     "pss_create", "pss_destroy", "pss_set_params", "pss_reset_history", "pss_set_history",
     "pss_set_position", "pss_enqueue", "pss_enqueue_ex", "pss_read_results", "pss_read_state",
     "pss_get_state_ptrs", "pss_sanitize_request", "pss_stream", "pss_status_string",
-    "pss_mask_words", "pss_set_score_targets", "pss_reset_gate",
+    "pss_mask_words", "pss_set_score_targets", "pss_reset_gate", "pss_enqueue_noalloc",
 ]
+NOALLOC_MAX_ROWS = 16
+
+
+def enqueue_noalloc(params_ptr, state, vocab, logits_ptr, dtype, row_stride, rows, mode=MODE_SAMPLE,
+                    do_increment=1, pass_idx=0, rng_mode=RNG_XORSHIFT32, max_topk=0, max_window=0,
+                    row_info=None, stream=None):
+    """pss_enqueue_noalloc: one step on caller-owned device buffers (state: a
+    dict of device pointers with the pss_state_ptrs fields)."""
+    sp = CStatePtrs(*[state[n] for n, _ in CStatePtrs._fields_])
+    o = CEnqueueOpts(row_info, None, None, 0, None, 0, None, 0, 0xFFFFFFFF) if row_info else None
+    _ok(lib().pss_enqueue_noalloc(params_ptr, ctypes.byref(sp), vocab, logits_ptr, dtype, row_stride, rows,
+                                  mode, do_increment, pass_idx, rng_mode, max_topk, max_window,
+                                  None if o is None else ctypes.byref(o), stream), "pss_enqueue_noalloc")
 
 
 class PssError(RuntimeError):
@@ -103,6 +116,7 @@ def lib():
         L.pss_read_results.argtypes = [P, u32, P, P]
         L.pss_read_state.argtypes = [P, u32, P, P, P, P]
         L.pss_get_state_ptrs.argtypes = [P, P]
+        L.pss_enqueue_noalloc.argtypes = [P, P, u32, P, u32, u64, u32, u32, u32, u32, u32, u32, u32, P, P]
         L.pss_sanitize_request.argtypes = [P, P]
         L.pss_stream.argtypes = [P]
         L.pss_stream.restype = P

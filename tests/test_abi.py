@@ -81,3 +81,14 @@ def test_null_handles_rejected_without_gpu():
     assert L.pss_create(None, 100, 1, None) == 1
     assert L.pss_create(ctypes.byref(h), 0, 1, None) == 1
     assert L.pss_create(ctypes.byref(h), S.MAX_VOCAB + 1, 1, None) == 4
+
+
+def test_noalloc_rejects_more_rows_than_its_workspace_without_gpu():
+    # checked on the host before any device call (the pointers are never used)
+    L = S.lib()
+    sp = S.CStatePtrs(*([16] * len(S.CStatePtrs._fields_)))
+    args = lambda rows: (16, ctypes.byref(sp), 1000, 16, S.DTYPE_F32, 1000, rows, S.MODE_SAMPLE, 1, 0,
+                         S.RNG_XORSHIFT32, 0, 0, None, None)
+    assert L.pss_enqueue_noalloc(*args(S.NOALLOC_MAX_ROWS + 1)) == 1
+    assert L.pss_enqueue_noalloc(*args(0)) == 1
+    assert L.pss_enqueue_noalloc(None, ctypes.byref(sp), 1000, 16, 0, 1000, 1, 1, 1, 0, 0, 0, 0, None, None) == 1
