@@ -21,11 +21,13 @@ A "step" is one pss_enqueue over a batch of logit rows resident in HBM.
   lmhead    the LM head before the sampler (RMSNorm + fp16 GEMV over a
             4,096 x 102,400 block-transposed head): us per call and HBM GB/s
             for 1 and 4 rows, logits and fused-greedy forms.
-  torch_sum_same_bytes  a library reduction (torch.sum, fp32) over the
-            same bytes as one headline batch, on the same box, for context
-            beside the kernels' HBM rates (run in a child process).
-  cpu_baseline  the O1 oracle (scalar C, sort-based) on the box's host cores
-            over a bounded sample of the headline rows.
+  read_ceiling  pss_read_ceiling: the resident kernel's access pattern with
+            nothing else, over the same bytes as one headline batch -- the
+            achievable read rate the sampler's fraction is set beside.
+  cpu_baseline  the O1 oracle (scalar C, sort-based) on the box's host cores,
+            one pinned thread per allowed CPU (up to 16), over a bounded
+            sample of the headline rows; one-thread and O3 (sampler_ref)
+            lines beside it.
 
 Prints ONE JSON line.  Algorithmic bytes per row = V*elem + 4*W + 44.
 """
@@ -254,63 +256,84 @@ def bench_lmhead(steps, K=4096, V=102400, rows_list=(1, 4)):
     return out
 
 
-_READ_CEILING = r"""
-import json, sys, torch
-nbytes, reps, nbuf = int(sys.argv[1]), int(sys.argv[2]), int(sys.argv[3])
-xs = [torch.ones(nbytes // 4, dtype=torch.float32, device="cuda") for _ in range(nbuf)]
-for i in range(5):
-    xs[i % nbuf].sum()
-torch.cuda.synchronize()
-e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-e0.record()
-for i in range(reps):
-    xs[i % nbuf].sum()
-e1.record()
-torch.cuda.synchronize()
-us = e0.elapsed_time(e1) * 1e3 / reps
-print(json.dumps({"bytes": nbytes, "us": us, "gbps": nbytes / (us * 1e-6) / 1e9,
-                  "how": "torch.sum over fp32, %d rotating buffers, child process" % nbuf}))
-"""
+def read_ceiling(nbytes, reps=100):
+    """The read ceiling: pss_read_ceiling (the resident kernel's access
+    pattern -- 1,024-thread workgroups over 400 KiB chunks, 16-byte
+    nontemporal loads -- and nothing else) over NBUF rotating buffers of
+    `nbytes`, back to back on one stream, bracketed by HIP events."""
+    from pumice_amd import hip
+    from pumice_amd import sampler as S
+
+    L = S.lib()
+    bufs = [hip.DeviceBuffer(nbytes) for _ in range(NBUF)]
+    for b in bufs:
+        b.fill_u32(0x3F800000)
+    nblk = int(L.pss_read_ceiling_blocks(nbytes))
+    out = hip.DeviceBuffer(4 * nblk)
+    try:
+        for i in range(10):
+            S._ok(L.pss_read_ceiling(bufs[i % NBUF].ptr, nbytes, out.ptr, None), "pss_read_ceiling")
+        hip.synchronize()
+        e0, e1 = hip.Event(), hip.Event()
+        e0.record(None)
+        for i in range(reps):
+            S._ok(L.pss_read_ceiling(bufs[i % NBUF].ptr, nbytes, out.ptr, None), "pss_read_ceiling")
+        e1.record(None)
+        hip.synchronize()
+        us = e0.elapsed_ms(e1) * 1e3 / reps
+    finally:
+        out.free()
+        for b in bufs:
+            b.free()
+    return {"bytes": nbytes, "us_per_launch": us, "gbps": nbytes / (us * 1e-6) / 1e9, "workgroups": nblk,
+            "how": "pss_read_ceiling, %d rotating buffers, %d launches back to back, HIP events" % (NBUF, reps)}
 
 
-def read_ceiling(nbytes, reps=50):
-    """torch's sum over a rotating set of fp32 tensors of `nbytes` each
-    (beyond the last-level cache), timed with torch events, in a child
-    process (torch brings its own HIP runtime, which does not share a process
-    with this library's)."""
-    import subprocess
-
-    r = subprocess.run([sys.executable, "-c", _READ_CEILING, str(nbytes), str(reps), str(NBUF)],
-                       capture_output=True, text=True, timeout=300)
-    if r.returncode != 0:
-        raise RuntimeError(r.stderr.strip().splitlines()[-1] if r.stderr.strip() else "child failed")
-    return json.loads(r.stdout.strip().splitlines()[-1])
+def _oracle_cflags():
+    try:
+        txt = open(os.path.join(ROOT, "oracle", "Makefile")).read()
+        line = txt.split("CFLAGS =", 1)[1].split("\n", 1)[0]
+        cont = txt.split("CFLAGS =", 1)[1].split("\n", 2)[1] if line.rstrip().endswith("\\") else ""
+        return "gcc " + " ".join((line.rstrip(" \\") + " " + cont).split())
+    except (OSError, IndexError):
+        return "unknown"
 
 
 def cpu_baseline(w, seconds):
-    """O1 (scalar C, sort-based restatement) on a bounded sample of the headline rows."""
+    """The reference's CPU path on the box's host cores over a bounded sample
+    of the headline rows: O1 (the scalar C restatement of the contract, a full
+    sort per row like the reference's sampler_ref) with one thread pinned to
+    each CPU this process may run on (capped at 16, the host share of one GPU
+    on these boxes), the same on one thread, and O3 (the restated sampler_ref
+    itself, src/validation.c:4974-5092, fp64) on all threads."""
     import oracle as O
 
-    def run(threads):
+    allowed = sorted(os.sched_getaffinity(0))
+    cpus = allowed[:16]
+
+    def run(kind, cp, budget):
         done, t0 = 0, time.perf_counter()
         while True:
             hist = w.history.copy()
             pos = np.zeros(w.rows, np.uint32)
             rng = w.seeds.copy()
             step = np.zeros(w.rows, np.uint32)
-            O.o1_batch(w.logits, w.params, hist, pos, rng, step, threads=threads)
+            O.batch_pinned(kind, w.logits, w.params, hist, pos, rng, step, cp)
             done += w.rows
             el = time.perf_counter() - t0
-            if el >= seconds:
+            if el >= budget:
                 return done / el, done
 
-    rps1, n1 = run(1)
-    cores = min(16, os.cpu_count() or 1)
-    rpsn, nn = run(cores)
-    return dict(value=rps1, unit="rows/s", cores=1, kind="port",
-                sample=f"{n1} headline rows (256 x 102,400 fp32, c2 chain) in >= {seconds:.0f} s, 1 thread",
-                all_cores=dict(value=rpsn, cores=cores, rows=nn),
-                cpu=_cpu_model())
+    rpsn, nn = run("o1", cpus, seconds)
+    rps1, n1 = run("o1", cpus[:1], seconds / 2)
+    rps3, n3 = run("o3", cpus, seconds / 2)
+    return dict(value=rpsn, unit="rows/s", cores=len(cpus), kind="port",
+                sample=f"{nn} headline rows (256 x 102,400 fp32, the headline params) in >= {seconds:.0f} s, "
+                       f"{len(cpus)} threads pinned one per CPU",
+                cpus_online=os.sysconf("SC_NPROCESSORS_ONLN"), cpus_allowed=len(allowed),
+                cpu=_cpu_model(), compiler=_oracle_cflags(),
+                one_thread=dict(value=rps1, rows=n1),
+                o3_sampler_ref=dict(value=rps3, rows=n3, cores=len(cpus), kind="port of src/validation.c:4974-5092"))
 
 
 def _cpu_model():
@@ -463,11 +486,9 @@ def main():
         log("lm head (K 4096 x V 102400)")
         extra["lmhead"] = bench_lmhead(args.lmhead_steps)
         log("lmhead", json.dumps(extra["lmhead"]))
-        try:
-            extra["torch_sum_same_bytes"] = read_ceiling(head.logits.nbytes)
-            log("torch.sum over one batch", json.dumps(extra["torch_sum_same_bytes"]))
-        except Exception as exc:  # torch without a device build: no line
-            log("torch.sum baseline unavailable:", exc)
+    log("read ceiling")
+    ceiling = read_ceiling(head.logits.nbytes)
+    log("read ceiling", json.dumps(ceiling))
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
@@ -511,6 +532,12 @@ def main():
         "hbm_gbps": h["wall_gbps"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic},
+        "read_ceiling_gbps": ceiling["gbps"],
+        "read_ceiling": ceiling,
+        "roofline_by_config": {
+            name: {"achieved": extra[name]["stream_gbps"], "frac": extra[name]["stream_gbps"] / HBM_PEAK_GBPS,
+                   "us_per_launch": extra[name]["stream_ms_per_launch"] * 1e3}
+            for name in ("c3", "c4", "c5") if name in extra},
         "cpu_baseline": cpu,
         "p50_us_per_token_b1": extra.get("latency_b1", {}).get("launch_to_token_us_p50"),
         "headline": h,

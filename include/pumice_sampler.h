@@ -259,6 +259,15 @@ pss_status pss_enqueue_noalloc(const sample_params* params, const pss_state_ptrs
  * (src/compute.c:113-114): penaltyLength clamped to 1024, seed 0 -> 1. */
 pss_status pss_sanitize_request(sample_params* params, uint32_t* seed);
 
+/* Measurement helper (no counterpart in the reference): the plain read of
+ * `bytes` (a multiple of 16, 16-byte aligned) with the resident sampler
+ * kernel's access pattern and nothing else -- 1,024-thread workgroups over
+ * 400 KiB chunks, 16-byte nontemporal loads -- writing one word per
+ * workgroup to out[pss_read_ceiling_blocks(bytes)].  Its rate is the read
+ * ceiling the sampler's roofline fraction is set beside. */
+uint32_t pss_read_ceiling_blocks(uint64_t bytes);
+pss_status pss_read_ceiling(const void* src, uint64_t bytes, uint32_t* out, void* hip_stream);
+
 /* Stream the sampler enqueues on (hipStream_t). */
 void* pss_stream(pss_sampler* s);
 

@@ -64,6 +64,10 @@ def lib():
         L.oracle_o1_row.argtypes = [P, u32, P, P, u32, u32, u32, u32, P, P, P, P, P]
         L.oracle_o1_batch.restype = None
         L.oracle_o1_batch.argtypes = [P, u32, u64, u32, u32, P, P, P, P, P, u32, u32, u32, P, P, i32]
+        L.oracle_o1_batch_pinned.restype = None
+        L.oracle_o1_batch_pinned.argtypes = [P, u32, u64, u32, u32, P, P, P, P, P, u32, u32, u32, P, i32, P]
+        L.oracle_o3_batch_pinned.restype = None
+        L.oracle_o3_batch_pinned.argtypes = [P, u64, u32, u32, P, P, P, P, P, i32, P]
         L.oracle_o2_shader_row.restype = u32
         L.oracle_o2_shader_row.argtypes = [P, u32, P, P, P, P, u32, P]
         L.oracle_o3_sampler_ref.restype = u32
@@ -205,6 +209,24 @@ def o1_batch(logits, params, history, position, rng, step, mode=1, rng_mode=0, d
                           _ptr(rng), _ptr(step), mode, rng_mode, do_increment, _ptr(tokens),
                           _ptr(infos), int(threads))
     return tokens, infos
+
+
+def batch_pinned(kind, logits, params, history, position, rng, step, cpus):
+    """The CPU baseline's batch: O1 ("o1") or O3 ("o3", fp32 rows) over all
+    rows, one thread per entry of `cpus`, thread i pinned to cpus[i].  State
+    arrays updated in place; returns the tokens."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    rows, V = x.shape
+    prm = np.ascontiguousarray(params, dtype=SAMPLE_PARAMS)
+    cp = np.ascontiguousarray(cpus, dtype=np.int32)
+    tokens = np.zeros(rows, np.uint32)
+    if kind == "o1":
+        lib().oracle_o1_batch_pinned(_ptr(x), 0, V, rows, V, _ptr(prm), _ptr(history), _ptr(position),
+                                     _ptr(rng), _ptr(step), 1, 0, 1, _ptr(tokens), cp.size, _ptr(cp))
+    else:
+        lib().oracle_o3_batch_pinned(_ptr(x), V, rows, V, _ptr(prm), _ptr(history), _ptr(position),
+                                     _ptr(rng), _ptr(tokens), cp.size, _ptr(cp))
+    return tokens
 
 
 def o1_score_row(logits, target):

@@ -24,10 +24,12 @@
  * shared deterministic math header, pinned by tests against libm and
  * published known-answer vectors.
  */
+#define _GNU_SOURCE /* pthread_setaffinity_np: the CPU baseline pins one thread per core */
 #include "pss_oracle.h"
 
 #include <math.h>
 #include <pthread.h>
+#include <sched.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -314,11 +316,35 @@ typedef struct {
     uint32_t* tokens;
     pss_row_info* infos;
     uint32_t r0, r1;
+    int cpu;  /* >= 0: pin the worker to this CPU */
+    int o3;   /* run O3 (sampler_ref) instead of O1 */
 } batch_job;
+
+static void pin_self(int cpu) {
+    if (cpu < 0) return;
+    cpu_set_t set;
+    CPU_ZERO(&set);
+    CPU_SET(cpu, &set);
+    (void)pthread_setaffinity_np(pthread_self(), sizeof set, &set);
+}
 
 static void* batch_worker(void* arg) {
     batch_job* b = (batch_job*)arg;
+    pin_self(b->cpu);
     float* row = NULL;
+    if (b->o3) {
+        /* O3 mutates its row: a private copy per row */
+        row = (float*)malloc(sizeof(float) * b->V);
+        for (uint32_t r = b->r0; r < b->r1; ++r) {
+            memcpy(row, (const float*)b->logits + (uint64_t)r * b->stride, sizeof(float) * b->V);
+            int tol = 0;
+            uint32_t tok = oracle_o3_sampler_ref(row, (int)b->V, &b->params[r], b->history + (uint64_t)r * O_MAX_PEN,
+                                                 &b->position[r], &b->rng[r], 0xFFFFFFFFu, 5e-4, &tol);
+            if (b->tokens) b->tokens[r] = tok;
+        }
+        free(row);
+        return NULL;
+    }
     if (b->dtype == PSS_DTYPE_F16) row = (float*)malloc(sizeof(float) * b->V);
     for (uint32_t r = b->r0; r < b->r1; ++r) {
         const float* l;
@@ -346,10 +372,38 @@ static void* batch_worker(void* arg) {
     return NULL;
 }
 
+static void run_batch(const void* logits, uint32_t dtype, uint64_t row_stride, uint32_t rows, uint32_t V,
+                      const sample_params* params, uint32_t* history, uint32_t* position, uint32_t* rng,
+                      uint32_t* step, uint32_t mode, uint32_t rng_mode, uint32_t do_increment,
+                      uint32_t* tokens, pss_row_info* infos, int threads, const int* cpus, int o3);
+
 void oracle_o1_batch(const void* logits, uint32_t dtype, uint64_t row_stride, uint32_t rows,
                      uint32_t V, const sample_params* params, uint32_t* history, uint32_t* position,
                      uint32_t* rng, uint32_t* step, uint32_t mode, uint32_t rng_mode,
                      uint32_t do_increment, uint32_t* tokens, pss_row_info* infos, int threads) {
+    run_batch(logits, dtype, row_stride, rows, V, params, history, position, rng, step, mode, rng_mode,
+              do_increment, tokens, infos, threads, NULL, 0);
+}
+
+void oracle_o1_batch_pinned(const void* logits, uint32_t dtype, uint64_t row_stride, uint32_t rows,
+                            uint32_t V, const sample_params* params, uint32_t* history, uint32_t* position,
+                            uint32_t* rng, uint32_t* step, uint32_t mode, uint32_t rng_mode,
+                            uint32_t do_increment, uint32_t* tokens, int threads, const int* cpus) {
+    run_batch(logits, dtype, row_stride, rows, V, params, history, position, rng, step, mode, rng_mode,
+              do_increment, tokens, NULL, threads, cpus, 0);
+}
+
+void oracle_o3_batch_pinned(const float* logits, uint64_t row_stride, uint32_t rows, uint32_t V,
+                            const sample_params* params, uint32_t* history, uint32_t* position,
+                            uint32_t* rng, uint32_t* tokens, int threads, const int* cpus) {
+    run_batch(logits, PSS_DTYPE_F32, row_stride, rows, V, params, history, position, rng, NULL, 1, 0, 1,
+              tokens, NULL, threads, cpus, 1);
+}
+
+static void run_batch(const void* logits, uint32_t dtype, uint64_t row_stride, uint32_t rows, uint32_t V,
+                      const sample_params* params, uint32_t* history, uint32_t* position, uint32_t* rng,
+                      uint32_t* step, uint32_t mode, uint32_t rng_mode, uint32_t do_increment,
+                      uint32_t* tokens, pss_row_info* infos, int threads, const int* cpus, int o3) {
     if (threads < 1) threads = 1;
     if ((uint32_t)threads > rows) threads = (int)rows;
     batch_job jobs[256];
@@ -373,8 +427,10 @@ void oracle_o1_batch(const void* logits, uint32_t dtype, uint64_t row_stride, ui
         b->infos = infos;
         b->r0 = (uint32_t)((uint64_t)rows * i / threads);
         b->r1 = (uint32_t)((uint64_t)rows * (i + 1) / threads);
+        b->cpu = cpus ? cpus[i] : -1;
+        b->o3 = o3;
     }
-    if (threads == 1) {
+    if (threads == 1 && !cpus) { /* pinning happens on a worker thread, never the caller's */
         batch_worker(&jobs[0]);
         return;
     }

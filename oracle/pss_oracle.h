@@ -37,6 +37,17 @@ void oracle_o1_batch(const void* logits, uint32_t dtype, uint64_t row_stride, ui
                      uint32_t* rng, uint32_t* step, uint32_t mode, uint32_t rng_mode,
                      uint32_t do_increment, uint32_t* tokens, pss_row_info* infos, int threads);
 
+/* The CPU baseline: O1 (no diagnostics) or O3 over rows, thread i pinned
+ * to cpus[i] (cpus may be NULL: no pinning).  O3 runs on a private copy of
+ * each row, without the tolerance acceptance test. */
+void oracle_o1_batch_pinned(const void* logits, uint32_t dtype, uint64_t row_stride, uint32_t rows,
+                            uint32_t V, const sample_params* params, uint32_t* history, uint32_t* position,
+                            uint32_t* rng, uint32_t* step, uint32_t mode, uint32_t rng_mode,
+                            uint32_t do_increment, uint32_t* tokens, int threads, const int* cpus);
+void oracle_o3_batch_pinned(const float* logits, uint64_t row_stride, uint32_t rows, uint32_t V,
+                            const sample_params* params, uint32_t* history, uint32_t* position,
+                            uint32_t* rng, uint32_t* tokens, int threads, const int* cpus);
+
 /* O2: literal restatement of ArgMax-Reduce.comp mode 1 (TS=1024 partition,
  * 28+28 bisection, fp32, libm expf, a fixed reduction association).
  * Mutates `logits` in place like the shader.  V must be a multiple of 4. */

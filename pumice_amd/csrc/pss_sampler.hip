@@ -457,3 +457,56 @@ extern "C" pss_status pss_enqueue_noalloc(const sample_params* params, const pss
      * that uses the workspace stays inside scratch */
     return pss_launch_rows(a, rows, max_topk, max_window, -1, st, NULL) == hipSuccess ? PSS_OK : PSS_ERR_HIP;
 }
+
+/* ------------------------------------------------------------------------ */
+/* read ceiling: the stream alone                                            */
+/* ------------------------------------------------------------------------ */
+
+/* The resident kernel's access pattern with nothing else: one 1,024-thread
+ * workgroup per 400 KiB chunk, each wave reading PSS_READ_NL contiguous KiB
+ * with 16-byte nontemporal buffer loads, PSS_RES_DEPTH of them in flight;
+ * the values are folded into one word per workgroup so that no load is
+ * dropped.  Bytes beyond `bytes` read as 0 (buffer bounds). */
+#define PSS_READ_NL 25
+__global__ void __launch_bounds__(1024) pss_read_kernel(const char* src, uint64_t bytes, uint32_t* out) {
+    constexpr int NL = PSS_READ_NL, D = PSS_RES_DEPTH;
+    const uint64_t chunk = (uint64_t)NL * 16u * 1024u;
+    const uint64_t off = (uint64_t)blockIdx.x * chunk;
+    const uint64_t left = bytes - off;
+    const int nrec = (int)(left < chunk ? left : chunk);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)(src + off), (short)0, nrec, PSS_BUF_DW3);
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t vb = (wave * (uint32_t)NL * 64u + lane) * 16u;
+    uint4 r[NL];
+    uint32_t acc = 0u;
+#pragma unroll
+    for (int j = 0; j < D; ++j)
+        r[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(vb + 1024u * j), 0, PSS_NT));
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        if (j + D < NL)
+            r[j + D] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(vb + 1024u * (j + D)), 0, PSS_NT));
+        acc ^= r[j].x ^ r[j].y ^ r[j].z ^ r[j].w;
+    }
+    acc = wave_max_u32(acc);
+    __shared__ uint32_t wv[16];
+    if (lane == 0u) wv[wave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0u) {
+        uint32_t x = 0u;
+        for (int w = 0; w < 16; ++w) x ^= wv[w];
+        out[blockIdx.x] = x;
+    }
+}
+
+extern "C" uint32_t pss_read_ceiling_blocks(uint64_t bytes) {
+    const uint64_t chunk = (uint64_t)PSS_READ_NL * 16u * 1024u;
+    return (uint32_t)((bytes + chunk - 1u) / chunk);
+}
+
+extern "C" pss_status pss_read_ceiling(const void* src, uint64_t bytes, uint32_t* out, void* hip_stream) {
+    if (!src || !out || bytes == 0 || (bytes & 15u) || ((uintptr_t)src & 15u)) return PSS_ERR_INVALID_ARG;
+    const uint32_t blocks = pss_read_ceiling_blocks(bytes);
+    pss_read_kernel<<<dim3(blocks), dim3(1024), 0, (hipStream_t)hip_stream>>>((const char*)src, bytes, out);
+    return hipGetLastError() == hipSuccess ? PSS_OK : PSS_ERR_HIP;
+}

@@ -71,6 +71,7 @@ EXPORTS = [
     "pss_set_position", "pss_enqueue", "pss_enqueue_ex", "pss_read_results", "pss_read_state",
     "pss_get_state_ptrs", "pss_sanitize_request", "pss_stream", "pss_status_string",
     "pss_mask_words", "pss_set_score_targets", "pss_reset_gate", "pss_enqueue_noalloc",
+    "pss_read_ceiling", "pss_read_ceiling_blocks",
 ]
 NOALLOC_MAX_ROWS = 16
 
@@ -116,6 +117,9 @@ def lib():
         L.pss_read_results.argtypes = [P, u32, P, P]
         L.pss_read_state.argtypes = [P, u32, P, P, P, P]
         L.pss_get_state_ptrs.argtypes = [P, P]
+        L.pss_read_ceiling.argtypes = [P, u64, P, P]
+        L.pss_read_ceiling_blocks.argtypes = [u64]
+        L.pss_read_ceiling_blocks.restype = u32
         L.pss_enqueue_noalloc.argtypes = [P, P, u32, P, u32, u64, u32, u32, u32, u32, u32, u32, u32, P, P]
         L.pss_sanitize_request.argtypes = [P, P]
         L.pss_stream.argtypes = [P]
@@ -126,7 +130,8 @@ def lib():
         L.pss_mask_words.restype = u32
         for n in EXPORTS:
             f = getattr(L, n)
-            if f.restype is ctypes.c_int and n not in ("pss_stream", "pss_status_string", "pss_mask_words"):
+            if f.restype is ctypes.c_int and n not in ("pss_stream", "pss_status_string", "pss_mask_words",
+                                                       "pss_read_ceiling_blocks"):
                 f.restype = i32
         _lib = L
     return _lib
