@@ -1605,10 +1605,12 @@ __global__ void __launch_bounds__(PSS_ST_NT) pss_fin_kernel(pss_args a, uint32_t
  * PSS_SEG_NW, in one round (each wave one item, the joint certificate over
  * the workgroup's items).  Pool entries and counts are agent-scope stores;
  * every wave waits for its stores to complete, then the workgroup counts
- * itself on the row's ticket (agent-scope atomic), and the workgroup that
- * completes the count resets it and finishes the row in place (pss_fin_row,
- * its scratch over the staging area).  One kernel, no cache-flushing fence,
- * no workgroup waits for another.
+ * itself on the row's ticket with an agent-scope acquire-release
+ * fetch-add (release: this workgroup's stores happen before its count;
+ * acquire: the workgroup that completes the count sees every other
+ * workgroup's stores), and that workgroup resets the ticket and finishes the
+ * row in place (pss_fin_row, its scratch over the staging area).  One
+ * kernel, no workgroup waits for another.
  */
 template <int EPT, int DT>
 union pss_small_scratch {
@@ -1635,7 +1637,7 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_small_kernel(pss_args a, uint3
     __syncthreads();
     if (tid == 0u) {
         pss_row_ws* ws = (pss_row_ws*)((char*)a.ws + (size_t)row * PSS_WS_ROW_BYTES);
-        const bool l = atomicAdd(&ws->ticket, 1u) == GW - 1u;
+        const bool l = __hip_atomic_fetch_add(&ws->ticket, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == GW - 1u;
         if (l) pss_st_agent(&ws->ticket, 0u); /* every other workgroup of the row has counted */
         last = l ? 1u : 0u;
     }
