@@ -61,7 +61,7 @@ struct plh_head {
     const float* gamma;
     uint32_t K, V, max_rows, ntiles;
     float* an;               /* [max_rows][K] normalized rows */
-    unsigned long long* win; /* [max_rows][PLH_WIN_ROW] greedy maxima, zero between calls */
+    unsigned long long* win; /* [max_rows][PLH_WIN_ROW] greedy maxima, zeroed at the start of each greedy call */
 };
 
 struct plh_args {
@@ -85,11 +85,16 @@ struct plh_args {
  * the four wave sums are added in wave order. */
 __global__ void __launch_bounds__(PLH_NORM_NT) plh_norm_kernel(const float* __restrict__ x, uint64_t xs,
                                                                const float* __restrict__ gamma,
-                                                               float* __restrict__ an, uint32_t K) {
+                                                               float* __restrict__ an, uint32_t K,
+                                                               unsigned long long* __restrict__ win) {
     constexpr uint32_t NB = 16;                 /* values per thread held in registers */
     constexpr uint32_t CH = PLH_NORM_NT * NB;   /* K up to CH: one load of x and gamma */
     __shared__ double wsum[PLH_NORM_NT / PSS_WAVE];
     const uint32_t row = blockIdx.x, t = threadIdx.x;
+    /* greedy calls: the row's maxima slots start at zero in every call (this
+     * kernel precedes the GEMV's atomics in stream order), whatever an
+     * earlier call left in them */
+    if (win && t < PLH_WIN_SLOTS) win[(size_t)row * PLH_WIN_ROW + t * PLH_WIN_STRIDE] = 0ull;
     const float* xr = x + (size_t)row * xs;
     float v[NB], gv[NB];
     double s = 0.0;
@@ -322,7 +327,8 @@ static inline int plh_pick_r(uint32_t rows) { return rows == 1u ? 1 : rows == 2u
 
 template <bool GREEDY>
 static pss_status plh_launch(plh_head* h, const float* x, uint64_t xs, uint32_t rows, plh_args a) {
-    hipLaunchKernelGGL(plh_norm_kernel, dim3(rows), dim3(PLH_NORM_NT), 0, h->stream, x, xs, h->gamma, h->an, h->K);
+    hipLaunchKernelGGL(plh_norm_kernel, dim3(rows), dim3(PLH_NORM_NT), 0, h->stream, x, xs, h->gamma, h->an, h->K,
+                       GREEDY ? h->win : (unsigned long long*)nullptr);
     const int R = plh_pick_r(rows);
     const dim3 grid(h->ntiles, (rows + (uint32_t)R - 1u) / (uint32_t)R);
     if (R == 1)
