@@ -28,6 +28,7 @@
 #include "pss_device.h"
 
 #define PSS_GEN_NT 1024
+#define PSS_GEN_U 8 /* ids per thread per pass step, loads requested together */
 #define PSS_NO_TOKEN 0xFFFFFFFFu
 
 /* Output stores of the epilogue: plain stores.  (Write-through agent-scope
@@ -198,11 +199,33 @@ __device__ __forceinline__ void pss_general_row(const pss_args& a, uint32_t row,
     auto T = [&](uint32_t j, uint32_t c0) -> float {
         return pss_transform(pss_load1(rowp, a.dtype, j), c.doPen && pss_bit(bits, j - c0), c);
     };
+    /* Unchunked passes take PSS_GEN_U ids per thread per step, their loads
+     * requested together (one memory round trip per step instead of per id);
+     * ids past V come as -inf with valid = false. */
+    constexpr int U = PSS_GEN_U;
+    auto each_step = [&](auto&& g) {
+        for (uint32_t j0 = 0; j0 < V; j0 += NT * (uint32_t)U) {
+            float x[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t j = j0 + (uint32_t)u * NT + tid;
+                x[u] = j < V ? pss_load1(rowp, a.dtype, j) : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t j = j0 + (uint32_t)u * NT + tid;
+                const bool valid = j < V;
+                g(j, valid ? pss_transform(x[u], c.doPen && pss_bit(bits, j), c) : pss_u2f(0xFF800000u), valid);
+            }
+        }
+    };
     /* One pass over the row: f(j, t) for every id, ids strided over threads.
      * Every thread of the workgroup calls it. */
     auto pass = [&](auto&& f) {
         if (!chunked) {
-            for (uint32_t j = tid; j < V; j += NT) f(j, T(j, 0u));
+            each_step([&](uint32_t j, float t, bool valid) {
+                if (valid) f(j, t);
+            });
             return;
         }
         for (uint32_t c0 = 0; c0 < V; c0 += CH) {
@@ -216,14 +239,121 @@ __device__ __forceinline__ void pss_general_row(const pss_args& a, uint32_t row,
     /* S3, and the smallest key: the radix selects start below the common
      * prefix of the range they search (none at all on an all-equal row) */
     uint64_t mk = 0, nk = 0;
-    pass([&](uint32_t, float t) {
-        const uint64_t k = pss_key(t);
-        mk = k > mk ? k : mk;
-        nk = (0xFFFFFFFFull ^ k) > nk ? (0xFFFFFFFFull ^ k) : nk;
-    });
+    constexpr uint32_t NWV = NT / PSS_WAVE;
+    const uint32_t lane = tid & 63u, wv = tid >> 6;
+    const uint32_t nblk = (V + 1023u) / 1024u;
+    static_assert(PSS_MAX_VOCAB <= 256u * 1024u, "per-block values fit the histogram");
+    static_assert(NT >= PSS_WAVE && 1024 % NT == 0, "whole waves; a block is whole workgroup passes");
+    if (!chunked) {
+        /* the row in 1,024-id blocks, block b taken by wave b % NW (lane l on
+         * ids 1024 b + 64 i + l: coalesced); each block's largest key and
+         * how many ids hold it go to sh.hist[b] (key << 32 | count) */
+        /* 16-byte aligned rows: the block as 16-byte loads, all in flight
+         * at once (4 per lane fp32, 2 fp16; lane l on 4 (8) consecutive ids) */
+        const bool vec = a.vec_ok && (V * (uint32_t)esz) % 16u == 0u;
+        for (uint32_t b = wv; b < nblk && vec; b += NWV) {
+            constexpr int NQ = 4;
+            const uint32_t per = a.dtype == PSS_DTYPE_F16 ? 8u : 4u; /* ids per 16-byte load */
+            const uint32_t nq = 1024u / (64u * per);                 /* loads per lane: 4 or 2 */
+            uint4 r[NQ];
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                const uint32_t j = b * 1024u + (uint32_t)q * 64u * per + lane * per;
+                r[q] = (uint32_t)q < nq && j < V ? *(const uint4*)((const char*)rowp + (size_t)j * esz)
+                                                 : make_uint4(0u, 0u, 0u, 0u);
+            }
+            uint32_t km = 0u, cm = 0u;
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                const uint32_t w[4] = {r[q].x, r[q].y, r[q].z, r[q].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t j = b * 1024u + (uint32_t)q * 64u * per + lane * per + (uint32_t)e;
+                    if ((uint32_t)q < nq && (uint32_t)e < per && j < V) {
+                        float x;
+                        if (a.dtype == PSS_DTYPE_F16) {
+                            const uint16_t h = (uint16_t)(w[e >> 1] >> ((e & 1) * 16));
+                            _Float16 hf;
+                            __builtin_memcpy(&hf, &h, 2);
+                            x = (float)hf;
+                        } else {
+                            x = __uint_as_float(w[e & 3]);
+                        }
+                        const uint32_t k = pss_key(pss_transform(x, c.doPen && pss_bit(bits, j), c));
+                        cm = k > km ? 1u : cm + (k == km ? 1u : 0u);
+                        km = k > km ? k : km;
+                        nk = (0xFFFFFFFFull ^ k) > nk ? (0xFFFFFFFFull ^ k) : nk;
+                    }
+                }
+            }
+            mk = km > mk ? km : mk;
+            const uint32_t M = wave_max_u32(km);
+            const uint32_t cnt = wave_sum_u32(km == M ? cm : 0u);
+            if (lane == 0u) sh.hist[b] = ((uint64_t)M << 32) | cnt;
+        }
+        for (uint32_t b = wv; b < nblk && !vec; b += NWV) {
+            uint32_t km = 0u, cm = 0u;
+            for (uint32_t i0 = 0; i0 < 16u; i0 += (uint32_t)U) {
+                float x[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const uint32_t j = b * 1024u + (i0 + (uint32_t)u) * 64u + lane;
+                    x[u] = j < V ? pss_load1(rowp, a.dtype, j) : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const uint32_t j = b * 1024u + (i0 + (uint32_t)u) * 64u + lane;
+                    if (j < V) {
+                        const uint32_t k = pss_key(pss_transform(x[u], c.doPen && pss_bit(bits, j), c));
+                        cm = k > km ? 1u : cm + (k == km ? 1u : 0u);
+                        km = k > km ? k : km;
+                        nk = (0xFFFFFFFFull ^ k) > nk ? (0xFFFFFFFFull ^ k) : nk;
+                    }
+                }
+            }
+            mk = km > mk ? km : mk;
+            const uint32_t M = wave_max_u32(km);
+            const uint32_t cnt = wave_sum_u32(km == M ? cm : 0u);
+            if (lane == 0u) sh.hist[b] = ((uint64_t)M << 32) | cnt;
+        }
+    } else {
+        pass([&](uint32_t, float t) {
+            const uint64_t k = pss_key(t);
+            mk = k > mk ? k : mk;
+            nk = (0xFFFFFFFFull ^ k) > nk ? (0xFFFFFFFFull ^ k) : nk;
+        });
+    }
     const uint32_t tmaxKey = (uint32_t)block_max_u64<NT>(mk, sh.red);
     const uint32_t tminKey = (uint32_t)(0xFFFFFFFFull ^ block_max_u64<NT>(nk, sh.red));
     const float tmax = pss_unkey(tmaxKey);
+    /* ids holding the row maximum, when at least K of them: then the top-k
+     * set is exactly those ids (the K-th largest is the maximum), top-p
+     * cannot cut below it, every one has p = 1 (>= minP), so they are the
+     * kept set and the draw picks the floor(target / q(1))-th of them in id
+     * order; no select and no mass pass */
+    uint64_t cntM = 0;
+    if (!chunked) {
+        uint64_t cl = 0;
+        for (uint32_t b = tid; b < nblk; b += NT)
+            cl += (uint32_t)(sh.hist[b] >> 32) == tmaxKey ? (uint32_t)sh.hist[b] : 0u;
+        cntM = block_sum_u64<NT>(cl, sh.red);
+    }
+    const bool topTie = !chunked && c.K >= 1u && cntM >= (uint64_t)c.K && (!c.useMinP || 1.0f >= c.minP);
+    /* p = exp(t - tmax) depends on the key alone: each thread keeps its last
+     * two keys' values (heavy ties then skip the exp; 0xFFFFFFFF is no key
+     * of a canonical value) */
+    uint32_t pk0 = 0xFFFFFFFFu, pk1 = 0xFFFFFFFFu;
+    float pv0 = 0.0f, pv1 = 0.0f;
+    auto prob_of = [&](float t, uint32_t k) -> float {
+        if (k == pk0) return pv0;
+        if (k == pk1) return pv1;
+        const float p = pss_prob(t, tmax);
+        pk1 = pk0;
+        pv1 = pv0;
+        pk0 = k;
+        pv0 = p;
+        return p;
+    };
 
     /* Radix select over the row: digit levels of 8 bits from the top.  weight
      * 0 = count (top-k), 1 = mass restricted to key >= lo (top-p).  Without
@@ -243,16 +373,14 @@ __device__ __forceinline__ void pss_general_row(const pss_args& a, uint32_t row,
             auto wof = [&](float t, uint32_t k) -> uint64_t {
                 if ((k & pmask) != prefix) return 0ull;
                 if (weight == 0) return 1ull;
-                return k >= lo ? pss_fixq(pss_prob(t, tmax)) : 0ull;
+                return k >= lo ? pss_fixq(prob_of(t, k)) : 0ull;
             };
             if (!chunked) {
-                for (uint32_t j0 = 0; j0 < V; j0 += NT) {
-                    const uint32_t j = j0 + tid;
-                    const float t = j < V ? T(j, 0u) : pss_u2f(0xFF800000u);
+                each_step([&](uint32_t, float t, bool valid) {
                     const uint32_t k = pss_key(t);
-                    const uint64_t w = j < V ? wof(t, k) : 0ull;
+                    const uint64_t w = valid ? wof(t, k) : 0ull;
                     pss_hist_add_wave(sh.hist, (k >> shift) & 255u, w, weight == 0);
-                }
+                });
             } else {
                 pass([&](uint32_t, float t) {
                     const uint32_t k = pss_key(t);
@@ -271,84 +399,238 @@ __device__ __forceinline__ void pss_general_row(const pss_args& a, uint32_t row,
         return prefix;
     };
 
+    /* q of p = 1 (the value of every id at the row maximum) */
+    const uint64_t q1 = pss_fixq(pss_prob(tmax, tmax));
     /* S5 */
-    const uint32_t tauK = c.K > 0u ? select(c.K, 0, 0u) : 0u;
-    uint64_t zl = 0;
-    pass([&](uint32_t, float t) {
-        if (pss_key(t) >= tauK) zl += pss_fixq(pss_prob(t, tmax));
-    });
-    const uint64_t zk = block_sum_u64<NT>(zl, sh.red);
-    /* S6 */
-    uint32_t tau = tauK;
-    if (c.useTopP) {
-        const uint32_t tauP = select(pss_topp_need(c.topP, zk), 1, tauK);
-        tau = tauP > tau ? tauP : tau;
+    uint32_t tauK = tmaxKey, tau = tmaxKey;
+    uint64_t zk = cntM * q1;
+    if (!topTie) {
+        tauK = c.K > 0u ? select(c.K, 0, 0u) : 0u;
+        uint64_t zl = 0;
+        pass([&](uint32_t, float t) {
+            const uint32_t k = pss_key(t);
+            if (k >= tauK) zl += pss_fixq(prob_of(t, k));
+        });
+        zk = block_sum_u64<NT>(zl, sh.red);
+        /* S6 */
+        tau = tauK;
+        if (c.useTopP) {
+            const uint32_t tauP = select(pss_topp_need(c.topP, zk), 1, tauK);
+            tau = tauP > tau ? tauP : tau;
+        }
     }
 
     /* S7 */
     auto kept_q = [&](float t, uint64_t* q, float* pout) -> bool {
-        const float p = pss_prob(t, tmax);
-        const bool k = pss_key(t) >= tau && (!c.useMinP || p >= c.minP);
+        const uint32_t key = pss_key(t);
+        const float p = key >= tau ? prob_of(t, key) : 0.0f;
+        const bool k = key >= tau && (!c.useMinP || p >= c.minP);
         *q = k ? pss_fixq(p) : 0;
         *pout = p;
         return k;
     };
-    uint64_t zs = 0;
-    uint32_t cnt = 0, lastKept = 0;
-    pass([&](uint32_t j, float t) {
-        uint64_t q;
-        float p;
-        if (kept_q(t, &q, &p)) {
-            zs += q;
-            cnt++;
-            lastKept = j + 1u;
-        }
-    });
-    const uint64_t Z = block_sum_u64<NT>(zs, sh.red);
-    const uint32_t keptCount = (uint32_t)block_sum_u64<NT>(cnt, sh.red);
-    const uint32_t lastAll = (uint32_t)block_max_u64<NT>(lastKept, sh.red);
-
-    /* S8: walk the row in id order, chunk by chunk; within a chunk each thread
-     * owns a contiguous id range and a block scan orders the ranges. */
     uint32_t newRng;
     const uint32_t u24 = pss_draw_u24(a, row, &newRng);
-    const uint64_t target = pss_draw_target(u24, Z);
-    if (tid == 0) sh.tok = PSS_NO_TOKEN;
-    __syncthreads();
+    uint64_t Z, target;
+    uint32_t keptCount, lastAll;
     const uint32_t CW = chunked ? CH : V;
-    uint64_t base = 0;
-    for (uint32_t c0 = 0; c0 < V; c0 += CW) {
-        const uint32_t c0b = chunked ? c0 : 0u;
-        if (chunked) build(c0);
-        const uint32_t c1 = V - c0 < CW ? V : c0 + CW;
-        const uint32_t per = (c1 - c0 + NT - 1u) / NT;
-        const uint32_t j0 = c0 + tid * per < c1 ? c0 + tid * per : c1;
-        const uint32_t j1 = j0 + per < c1 ? j0 + per : c1;
-        uint64_t S = 0;
-        for (uint32_t j = j0; j < j1; ++j) {
-            uint64_t q;
-            float p;
-            if (kept_q(T(j, c0b), &q, &p)) S += q;
-        }
-        uint64_t tot;
-        const uint64_t P = block_excl_scan_u64<NT>(S, sh.red, &tot);
-        if (S > 0 && base + P <= target && target < base + P + S) {
-            uint64_t acc = base + P;
-            for (uint32_t j = j0; j < j1; ++j) {
-                uint64_t q;
-                float p;
-                if (kept_q(T(j, c0b), &q, &p)) {
-                    acc += q;
-                    if (acc > target) {
-                        sh.tok = j;
-                        break;
+    if (topTie) {
+        Z = zk;
+        keptCount = (uint32_t)cntM;
+        lastAll = 0u;
+        target = pss_draw_target(u24, Z);
+        const uint64_t nth = target / q1; /* the kept id the draw lands on, counted from 0 */
+        /* wave 0: the block holding it (per-block counts of the maximum) */
+        if (tid < PSS_WAVE) {
+            uint64_t c4[4], s4 = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t b = 4u * lane + (uint32_t)k;
+                c4[k] = b < nblk && (uint32_t)(sh.hist[b] >> 32) == tmaxKey ? (uint32_t)sh.hist[b] : 0u;
+                s4 += c4[k];
+            }
+            uint64_t base = wave_incl_scan_u64(s4) - s4;
+            if (lane == 0u) {
+                sh.tok = PSS_NO_TOKEN;
+                sh.digit = PSS_NO_TOKEN;
+            }
+            if (s4 > 0 && base <= nth && nth < base + s4) {
+                uint32_t blk = PSS_NO_TOKEN;
+                uint64_t bbase = 0;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if (blk == PSS_NO_TOKEN && c4[k] > 0 && nth < base + c4[k]) {
+                        blk = 4u * lane + (uint32_t)k;
+                        bbase = base;
                     }
+                    base += c4[k];
                 }
+                sh.digit = blk;
+                sh.rem = nth - bbase;
             }
         }
         __syncthreads();
-        base += tot;
-        if (sh.tok != PSS_NO_TOKEN || base > target) break;
+        const uint32_t blk = sh.digit;
+        if (blk != PSS_NO_TOKEN) {
+            /* the block's ids in order: the (rem)-th holding the maximum */
+            uint64_t seen = 0;
+            const uint64_t want = sh.rem;
+            for (uint32_t sub = 0; sub < 1024u; sub += NT) {
+                const uint32_t j = blk * 1024u + sub + tid;
+                const uint64_t f = j < V && pss_key(T(j, 0u)) == tmaxKey ? 1u : 0u;
+                uint64_t tot;
+                const uint64_t P = block_excl_scan_u64<NT>(f, sh.red, &tot);
+                if (f && seen + P == want) sh.tok = j;
+                seen += tot;
+                __syncthreads();
+            }
+        }
+        __syncthreads();
+    } else if (!chunked) {
+        /* S7 and S8 together.  The row in 1,024-id blocks, block b taken by
+         * wave b % NW (lane l on ids 1024 b + 64 i + l: coalesced), each
+         * block's kept mass recorded in sh.hist (V <= 256 blocks); Z is their
+         * sum; the block holding the draw target comes from a scan over the
+         * block masses, then the block's ids are scanned in order. */
+        uint64_t zs = 0;
+        uint32_t cnt = 0, lastKept = 0;
+        for (uint32_t b = wv; b < nblk; b += NWV) {
+            uint64_t bs = 0;
+            for (uint32_t i0 = 0; i0 < 16u; i0 += (uint32_t)U) {
+                float x[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const uint32_t j = b * 1024u + (i0 + (uint32_t)u) * 64u + lane;
+                    x[u] = j < V ? pss_load1(rowp, a.dtype, j) : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const uint32_t j = b * 1024u + (i0 + (uint32_t)u) * 64u + lane;
+                    uint64_t q;
+                    float p;
+                    if (j < V && kept_q(pss_transform(x[u], c.doPen && pss_bit(bits, j), c), &q, &p)) {
+                        bs += q;
+                        cnt++;
+                        lastKept = j + 1u;
+                    }
+                }
+            }
+            zs += bs;
+            bs = wave_sum_u64(bs);
+            if (lane == 0u) sh.hist[b] = bs;
+        }
+        Z = block_sum_u64<NT>(zs, sh.red);
+        keptCount = (uint32_t)block_sum_u64<NT>(cnt, sh.red);
+        lastAll = (uint32_t)block_max_u64<NT>(lastKept, sh.red);
+        target = pss_draw_target(u24, Z);
+        /* wave 0: lane l sums blocks 4l..4l+3; the lane whose range holds the
+         * target finds the block */
+        if (tid < PSS_WAVE) {
+            uint64_t m4[4], s4 = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t b = 4u * lane + (uint32_t)k;
+                m4[k] = b < nblk ? sh.hist[b] : 0ull;
+                s4 += m4[k];
+            }
+            uint64_t base = wave_incl_scan_u64(s4) - s4;
+            uint32_t blk = PSS_NO_TOKEN;
+            uint64_t bbase = 0;
+            if (s4 > 0 && base <= target && target < base + s4) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if (blk == PSS_NO_TOKEN && m4[k] > 0 && target < base + m4[k]) {
+                        blk = 4u * lane + (uint32_t)k;
+                        bbase = base;
+                    }
+                    base += m4[k];
+                }
+            }
+            const uint64_t hit = __ballot(blk != PSS_NO_TOKEN);
+            if (lane == 0u) {
+                sh.tok = PSS_NO_TOKEN;
+                sh.digit = hit ? 0u : PSS_NO_TOKEN;
+            }
+            if (blk != PSS_NO_TOKEN) {
+                sh.digit = blk;
+                sh.rem = bbase;
+            }
+        }
+        __syncthreads();
+        const uint32_t blk = sh.digit;
+        const uint64_t bbase = sh.rem;
+        if (blk != PSS_NO_TOKEN) {
+            /* the block's ids in order, NT at a time, one per thread */
+            uint64_t base = bbase;
+            for (uint32_t sub = 0; sub < 1024u; sub += NT) {
+                const uint32_t j = blk * 1024u + sub + tid;
+                uint64_t q = 0;
+                float p;
+                if (j < V && !kept_q(T(j, 0u), &q, &p)) q = 0;
+                uint64_t tot;
+                const uint64_t P = block_excl_scan_u64<NT>(q, sh.red, &tot);
+                if (q > 0 && base + P <= target && target < base + P + q) sh.tok = j;
+                base += tot;
+                __syncthreads();
+            }
+        }
+        __syncthreads();
+    } else {
+        uint64_t zs = 0;
+        uint32_t cnt = 0, lastKept = 0;
+        pass([&](uint32_t j, float t) {
+            uint64_t q;
+            float p;
+            if (kept_q(t, &q, &p)) {
+                zs += q;
+                cnt++;
+                lastKept = j + 1u;
+            }
+        });
+        Z = block_sum_u64<NT>(zs, sh.red);
+        keptCount = (uint32_t)block_sum_u64<NT>(cnt, sh.red);
+        lastAll = (uint32_t)block_max_u64<NT>(lastKept, sh.red);
+
+        /* S8: walk the row in id order, chunk by chunk; within a chunk each
+         * thread owns a contiguous id range and a block scan orders the
+         * ranges. */
+        target = pss_draw_target(u24, Z);
+        if (tid == 0) sh.tok = PSS_NO_TOKEN;
+        __syncthreads();
+        uint64_t base = 0;
+        for (uint32_t c0 = 0; c0 < V; c0 += CW) {
+            const uint32_t c0b = c0;
+            build(c0);
+            const uint32_t c1 = V - c0 < CW ? V : c0 + CW;
+            const uint32_t per = (c1 - c0 + NT - 1u) / NT;
+            const uint32_t j0 = c0 + tid * per < c1 ? c0 + tid * per : c1;
+            const uint32_t j1 = j0 + per < c1 ? j0 + per : c1;
+            uint64_t S = 0;
+            for (uint32_t j = j0; j < j1; ++j) {
+                uint64_t q;
+                float p;
+                if (kept_q(T(j, c0b), &q, &p)) S += q;
+            }
+            uint64_t tot;
+            const uint64_t P = block_excl_scan_u64<NT>(S, sh.red, &tot);
+            if (S > 0 && base + P <= target && target < base + P + S) {
+                uint64_t acc = base + P;
+                for (uint32_t j = j0; j < j1; ++j) {
+                    uint64_t q;
+                    float p;
+                    if (kept_q(T(j, c0b), &q, &p)) {
+                        acc += q;
+                        if (acc > target) {
+                            sh.tok = j;
+                            break;
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+            base += tot;
+            if (sh.tok != PSS_NO_TOKEN || base > target) break;
+        }
     }
     uint32_t tok = sh.tok;
     uint32_t flags = 0;
