@@ -43,7 +43,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
-TRAFFIC_MD = "row_kernel_traffic_headline.md"
+TRAFFIC_MD = "sampler_traffic_by_config.md"
 NBUF = 6
 
 
@@ -346,69 +346,122 @@ def _cpu_model():
     return "unknown"
 
 
-def traffic_from_pmc(fetch_dir, write_dir, out_path, kname="pss_res_kernel"):
-    """HBM bytes per launch of the sampler kernels from two rocprofv3 --pmc runs
-    of `bench.py --no-extra --no-cpu-baseline --copy-calib` (FETCH_SIZE, then
-    WRITE_SIZE; counters in KiB per dispatch).  Each counter is scaled by what it
-    reads for the calibration copy (a device-to-device copy of one headline
-    batch: that many bytes read and written)."""
+SECTIONS = ("headline", "c3", "c4", "c5", "b1")
+
+
+def traffic_from_pmc(fetch_dir, write_dir, out_path):
+    """HBM bytes per launch of the sampler kernels, per bench section, from two
+    rocprofv3 --pmc runs of `bench.py --no-cpu-baseline --copy-calib`
+    (FETCH_SIZE, then WRITE_SIZE; counters in KiB per dispatch).
+
+    With --copy-calib the bench follows each section (headline, c3, c4, c5,
+    batch 1) with ten device-to-device copies of one headline batch: those
+    copies split the dispatch sequence into sections, and their known traffic
+    (that many bytes read and written) scales each counter.  A section's
+    launches are the dispatches of its most frequent sampler kernel; its bytes
+    per launch are the sum over all its sampler dispatches / launches."""
     import csv
     import glob
-
-    def per_kernel(d, counter):
-        files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
-        vals = {}
-        for fn in files:
-            for r in csv.DictReader(open(fn)):
-                if r["Counter_Name"] == counter:
-                    vals.setdefault((r["Kernel_Name"], int(r["Grid_Size"])), []).append(float(r["Counter_Value"]))
-        return vals
+    import re
+    from pumice_amd import workloads as WL
 
     nbytes = 256 * 102400 * 4
-    out = {}
+
+    def dispatches(d, counter):
+        out = []
+        for fn in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(fn)):
+                if r["Counter_Name"] == counter:
+                    out.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+        out.sort()
+        return out
+
+    def short(k):
+        m = re.search(r"(pss_\w+|plh_\w+)(<[^>]*>)?", k)
+        return (m.group(1) + (m.group(2) or "")) if m else k
+
+    def is_calib(k, v):
+        return "copyBuffer" in k and v * 1024 > nbytes / 4
+
+    def is_sampler(k):
+        s = short(k)
+        return s.startswith("pss_") and not s.startswith(("pss_fill_u32", "pss_read_kernel"))
+
+    per = {}
     for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
-        vals = per_kernel(d, counter)
-        copy = [v for (k, g), vs in vals.items() if "copyBuffer" in k for v in vs if v * 1024 > nbytes / 4]
+        seq = dispatches(d, counter)
+        copy = [v for _, k, v in seq if is_calib(k, v)]
         if not copy:
             raise SystemExit(f"{d}: no calibration copy dispatch found")
         scale = nbytes / (float(np.mean(copy)) * 1024.0)
-        out[counter] = {"copy_kib": float(np.mean(copy)), "scale": scale}
-        for (k, g), vs in vals.items():
-            if kname in k:
-                out[counter]["row_kib"] = float(np.mean(vs))
-                out[counter]["row_bytes"] = float(np.mean(vs)) * 1024.0 * scale
-    row = out["FETCH_SIZE"]["row_bytes"] + out["WRITE_SIZE"]["row_bytes"]
-    res = {"kernel": kname, "workload": "headline 256 x 102,400 fp32", "calibration_copy_bytes": nbytes,
-           "counters": out, "row_kernel_hbm_bytes_per_launch": row}
-    fc, wc = out["FETCH_SIZE"], out["WRITE_SIZE"]
+        segs, cur = [], []
+        for _, k, v in seq:
+            if is_calib(k, v):
+                if cur:
+                    segs.append(cur)
+                cur = []
+            elif is_sampler(k):
+                cur.append((short(k), v))
+        if cur:
+            segs.append(cur)
+        per[counter] = {"copy_kib": float(np.mean(copy)), "scale": scale, "segments": segs}
+    nseg = len(per["FETCH_SIZE"]["segments"])
+    if nseg != len(per["WRITE_SIZE"]["segments"]) or nseg > len(SECTIONS):
+        raise SystemExit("the two runs do not have the same sections")
+    gens = {"headline": lambda: WL.headline(seed=0), "c3": lambda: WL.c3(seed=3), "c4": lambda: WL.c4(seed=4),
+            "c5": lambda: WL.c5(seed=5), "b1": lambda: WL.c2(seed=2, rows=1, steps=1)[0]}
+    sections = {}
+    for i in range(nseg):
+        name = SECTIONS[i]
+        w = gens[name]()
+        entry = {"algorithmic_bytes_per_launch": int(w.bytes_per_row() * w.rows)}
+        total = 0.0
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            seg = per[counter]["segments"][i]
+            counts = {}
+            for k, v in seg:
+                counts[k] = counts.get(k, 0) + 1
+            launches = max(counts.values())
+            kib = sum(v for _, v in seg) / launches
+            entry[counter] = {"kib_per_launch": kib, "launches": launches}
+            entry["kernels"] = sorted(counts)
+            total += kib * 1024.0 * per[counter]["scale"]
+        entry["hbm_bytes_per_launch"] = total
+        entry["ratio"] = total / entry["algorithmic_bytes_per_launch"]
+        sections[name] = entry
+    head = sections["headline"]
+    res = {"kernel": head["kernels"][0].split("<")[0], "workload": "headline 256 x 102,400 fp32",
+           "calibration_copy_bytes": nbytes,
+           "scale": {c: per[c]["scale"] for c in per}, "copy_kib": {c: per[c]["copy_kib"] for c in per},
+           "sections": sections, "row_kernel_hbm_bytes_per_launch": head["hbm_bytes_per_launch"]}
     md = [
-        "# HBM traffic of %s, headline workload (256 x 102,400 fp32)" % kname,
+        "# HBM traffic of the sampler kernels, per bench configuration",
         "",
         "Commands (from the repository root on the MI355X box; then, on any host,",
         "`python3 bench.py --traffic-from <fetch dir> <write dir>` wrote this file):",
         "",
         "    cd /tmp && export TMPDIR=/tmp",
-        "    timeout -s KILL 90 rocprofv3 --pmc FETCH_SIZE -d $REPO/gpurun_out/prof_fetch -o run --output-format csv \\",
-        "        -- python3 $REPO/bench.py --no-extra --no-cpu-baseline --steps 10 --warmup 2 --copy-calib",
-        "    timeout -s KILL 90 rocprofv3 --pmc WRITE_SIZE -d $REPO/gpurun_out/prof_write -o run --output-format csv \\",
-        "        -- python3 $REPO/bench.py --no-extra --no-cpu-baseline --steps 10 --warmup 2 --copy-calib",
+        "    timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE -d $REPO/gpurun_out/prof_fetch -o run --output-format csv \\",
+        "        -- python3 $REPO/bench.py --no-cpu-baseline --steps 10 --warmup 2 --latency-steps 20 --copy-calib",
+        "    timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE -d $REPO/gpurun_out/prof_write -o run --output-format csv \\",
+        "        -- python3 $REPO/bench.py --no-cpu-baseline --steps 10 --warmup 2 --latency-steps 20 --copy-calib",
         "",
-        "Calibration: a device-to-device copy of one batch (%d bytes read and written) reads"
+        "Calibration: a device-to-device copy of one headline batch (%d bytes read and written) reads"
         % nbytes,
         "FETCH_SIZE %.1f KiB and WRITE_SIZE %.1f KiB per dispatch, so the counters are scaled by %.4f and %.4f."
-        % (fc["copy_kib"], wc["copy_kib"], fc["scale"], wc["scale"]),
+        % (per["FETCH_SIZE"]["copy_kib"], per["WRITE_SIZE"]["copy_kib"], per["FETCH_SIZE"]["scale"],
+           per["WRITE_SIZE"]["scale"]),
+        "Algorithmic bytes per launch: rows x (V x element size + 4 x window + 44).",
         "",
-        "| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes per launch (scaled) |",
-        "|---|---|---|---|",
-        "| %s | %.1f | %.1f | %.0f |" % (kname, fc["row_kib"], wc["row_kib"], row),
-        "",
-        "Algorithmic bytes per launch: 256 x (102,400 x 4 + 4 x 64 + 44) = %d." % (256 * (409600 + 256 + 44)),
-        "",
-        "```json",
-        json.dumps(res, indent=1),
-        "```",
-        "",
+        "| config | kernels | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes per launch (scaled) | algorithmic | ratio |",
+        "|---|---|---|---|---|---|---|",
     ]
+    for name, e in sections.items():
+        md.append("| %s | %s | %.1f | %.1f | %.0f | %d | %.3f |" % (
+            name, ", ".join("`%s`" % k for k in e["kernels"]), e["FETCH_SIZE"]["kib_per_launch"],
+            e["WRITE_SIZE"]["kib_per_launch"], e["hbm_bytes_per_launch"], e["algorithmic_bytes_per_launch"],
+            e["ratio"]))
+    md += ["", "```json", json.dumps(res, indent=1), "```", ""]
     with open(out_path, "w") as f:
         f.write("\n".join(md))
     print(json.dumps(res))
@@ -480,9 +533,13 @@ def main():
             log("workload", name)
             extra[name] = bench_batched(gen(), max(args.steps // 2, 10), args.warmup, flags)
             log(name, json.dumps(extra[name]))
+            if args.copy_calib:
+                copy_calibration(head.logits.nbytes)
         log("latency (batch 1)")
         extra["latency_b1"] = bench_latency(args.latency_steps)
         log("latency", json.dumps(extra["latency_b1"]))
+        if args.copy_calib:
+            copy_calibration(head.logits.nbytes)
         log("lm head (K 4096 x V 102400)")
         extra["lmhead"] = bench_lmhead(args.lmhead_steps)
         log("lmhead", json.dumps(extra["lmhead"]))
@@ -496,6 +553,7 @@ def main():
         log("cpu", json.dumps(cpu))
 
     traffic = None
+    traffic_by = {}
     tpath = os.path.join(ROOT, "profiles", TRAFFIC_MD)
     if os.path.exists(tpath):
         with open(tpath) as f:
@@ -506,6 +564,7 @@ def main():
             kname = {"resident": "pss_res_kernel", "fused": "pss_row_kernel"}.get(kernel)
             if tj.get("kernel") == kname:
                 traffic = tj.get("row_kernel_hbm_bytes_per_launch")
+                traffic_by = {n: e["hbm_bytes_per_launch"] for n, e in tj.get("sections", {}).items()}
     # dominant (fused: only) kernel: algorithmic bytes per launch / mean
     # per-launch time from HIP events on the sampler's stream bracketing the
     # timed back-to-back launches (events around single launches, which add
@@ -536,7 +595,8 @@ def main():
         "read_ceiling": ceiling,
         "roofline_by_config": {
             name: {"achieved": extra[name]["stream_gbps"], "frac": extra[name]["stream_gbps"] / HBM_PEAK_GBPS,
-                   "us_per_launch": extra[name]["stream_ms_per_launch"] * 1e3}
+                   "us_per_launch": extra[name]["stream_ms_per_launch"] * 1e3,
+                   "traffic": traffic_by.get(name)}
             for name in ("c3", "c4", "c5") if name in extra},
         "cpu_baseline": cpu,
         "p50_us_per_token_b1": extra.get("latency_b1", {}).get("launch_to_token_us_p50"),

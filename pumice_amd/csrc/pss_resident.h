@@ -36,7 +36,7 @@
 #ifndef PSS_RESIDENT_H
 #define PSS_RESIDENT_H
 
-#include "pss_stream.h"
+#include "pss_wide.h"
 
 #define PSS_RES_NW 16
 #define PSS_RES_NT (PSS_RES_NW * PSS_WAVE)
@@ -72,42 +72,6 @@ struct pss_res_shared {
     uint32_t G;                                        /* the bound */
     uint32_t over;                                     /* a wave's range holds more window ids than it keeps */
 };
-
-/* Value e of a load as a transformed float: fp32 loads hold t in place; fp16
- * loads hold the raw halves (excluded elements set to -inf). */
-template <int DT>
-__device__ __forceinline__ float pss_res_t(const uint4& r, int e, float invT) {
-    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-    if (DT == PSS_DTYPE_F16) {
-        const uint16_t h = (uint16_t)(w[e >> 1] >> ((e & 1) * 16));
-        _Float16 hf;
-        __builtin_memcpy(&hf, &h, 2);
-        return (float)hf * invT;
-    }
-    return __uint_as_float(w[e]);
-}
-
-/* Element e of a load set to -inf (an excluded id). */
-template <int DT>
-__device__ __forceinline__ void pss_res_kill(uint4& r, int e) {
-    uint32_t w[4] = {r.x, r.y, r.z, r.w};
-    if (DT == PSS_DTYPE_F16)
-        w[e >> 1] = (w[e >> 1] & ~(0xFFFFu << ((e & 1) * 16))) | (0xFC00u << ((e & 1) * 16));
-    else
-        w[e] = 0xFF800000u;
-    r = make_uint4(w[0], w[1], w[2], w[3]);
-}
-
-/* x as a uniform value defined at this point of the instruction stream (the
- * compiler places no use of x, and no wait for the load that produced it,
- * before this point). */
-template <class T>
-__device__ __forceinline__ void pss_pin_s(T& x) {
-    static_assert(sizeof(T) == 4, "32-bit values");
-    uint32_t u = __builtin_bit_cast(uint32_t, x);
-    __asm__ __volatile__("" : "+v"(u));
-    x = __builtin_bit_cast(T, __builtin_amdgcn_readfirstlane(u));
-}
 
 template <int NL, int DT>
 __global__ void __launch_bounds__(PSS_RES_NT) pss_res_kernel(pss_args a, const sample_params* __restrict__ params) {
@@ -510,6 +474,11 @@ static inline hipError_t pss_launch_rows(pss_args a, uint32_t rows, uint32_t max
     const bool vec = ((a.stride * esz) % 16u == 0u) && (((uintptr_t)a.logits & 15u) == 0u) &&
                      ((a.V * esz) % 16u == 0u);
     const bool fits = vec && pss_res_pick_nl(a.V, (uint32_t)esz) != 0;
+    /* wide launches (top-k above PSS_SEG_KMAX or a window above
+     * PSS_SEG_WMAX ids): the split-row wide form where rows are 16-byte
+     * aligned, the wide fused form when asked for or otherwise */
+    if (form < 0 && vec && (max_k > PSS_SEG_KMAX || max_w > PSS_SEG_WMAX) && pss_wsplit_segments(a.V))
+        return pss_wsplit_launch(a, rows, st);
     if (form == PSS_FORM_RESIDENT || form < 0) {
         bool use = form == PSS_FORM_RESIDENT && fits;
         if (form < 0 && fits && max_k <= PSS_SEG_KMAX && max_w <= PSS_SEG_WMAX) {

@@ -132,6 +132,37 @@ def test_wide_fused(case, flags):
              step_logits=[logits, np.roll(logits, 3, axis=1)], where=f"wide {case}")
 
 
+@pytest.mark.parametrize("V", [248320, 248324, 131072, 65540])
+def test_wide_split_mixed_rows(V):
+    """The split-row wide form (auto choice for top-k above 256 or windows
+    above 256 ids) on one launch mixing row kinds: top-k 1,000 / 300 / 1,024,
+    top-k off (general algorithm in the finishing workgroup), greedy rows
+    (temperature 0), no window, a row whose window repeats one id, a row of
+    16 distinct values (bins of thousands of equal keys: the list finisher)
+    and a row rounded to 1/64 (a few equal keys per bin: the histogram
+    finisher's in-bin ranks); V with a partial last segment (248,324:
+    51,716 ids in segment 3; 65,540: a second segment of 4 ids) or exact
+    segments (131,072)."""
+    rng = np.random.default_rng(V)
+    rows = 10
+    logits = rng.normal(0.0, 3.0, (rows, V)).astype(np.float32)
+    logits[8] = np.sort(rng.normal(0.0, 3.0, 16)).astype(np.float32)[rng.integers(0, 16, V)]
+    logits[9] = np.round(logits[9] * 64.0) / 64.0
+    params = O.make_params(temperature=1.0, repPenalty=1.05, presencePenalty=0.2, penaltyLength=512, topK=1000,
+                           topP=0.99, minP=0.01, rows=rows)
+    params["topK"] = np.array([1000, 300, 1024, 0, 1000, 1000, 700, 1000, 1000, 900], np.uint32)
+    params["temperature"][4] = 0.0
+    params["penaltyLength"][5] = 0
+    params["topP"][6] = 1.0
+    params["minP"][7] = 0.0
+    hist = O.new_history(rows)
+    for r in range(rows):
+        hist[r, :512] = rng.integers(0, V, 512).astype(np.uint32)
+    hist[7, :512] = np.uint32(V - 1)
+    run_both(logits, params, np.arange(1, rows + 1, dtype=np.uint32), hist, None, steps=2,
+             step_logits=[logits, np.roll(logits, 5, axis=1)], where=f"wide split V={V}")
+
+
 FULL_BATCHES = {
     # name: (generator, rows) -- row counts that select each fast-kernel shape
     "headline_256x102400_f32": (lambda: WL.headline(seed=31), None),   # 512 x 200, one segment
