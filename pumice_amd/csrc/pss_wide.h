@@ -103,10 +103,11 @@ struct pss_wsp_geom {
 };
 
 /* ------------------------------------------------------------------------ */
-/* histogram finisher: up to 2,048 candidates, top-k up to 1,024             */
+/* histogram finisher: up to 4,096 candidates, top-k up to 1,024             */
 /* ------------------------------------------------------------------------ */
 
-#define PSS_HF_N 2048u    /* candidates the histogram finisher takes (two per thread of 1,024) */
+#define PSS_HF_N 4096u    /* candidates the histogram finisher takes (four per thread of 1,024) */
+#define PSS_HF_R 4        /* entries per thread */
 #define PSS_HF_BINS 2048u /* key bins: 11 bits below the common prefix of the bound and the maximum */
 #define PSS_HF_GATHER 64u /* entries of one bin resolved exactly by one wave */
 
@@ -159,7 +160,7 @@ __device__ __forceinline__ uint32_t pss_hf_digit512(const uint64_t* h, uint64_t&
 /*
  * Finisher over n <= PSS_HF_N candidates (list: key << 32 | id, in LDS), all
  * at or above `lo`, a lower bound of the row's K-th largest value, with the
- * row maximum tmaxKey among them; 1,024 threads, two entries each:
+ * row maximum tmaxKey among them; 1,024 threads, four entries each:
  *   1. one pass: each entry's count and mass q = fixq(p) into 2,048 bins of
  *      its key (the 11 bits below the common prefix of lo and tmaxKey, so
  *      bins are in key order); a block scan of the bins from the top;
@@ -179,7 +180,8 @@ __device__ __forceinline__ uint32_t pss_hf_digit512(const uint64_t* h, uint64_t&
  */
 __device__ __forceinline__ bool pss_hist_finish(const pss_args& a, uint32_t row, const pss_rowcfg& c,
                                                 const unsigned long long* list, uint32_t n, uint32_t lo,
-                                                uint32_t tmaxKey, pss_hfin_shared& hs) {
+                                                uint32_t tmaxKey, const pss_row_pre& pre, pss_hfin_shared& hs) {
+    constexpr int HR = PSS_HF_R;
     constexpr int NT = PSS_WSP_NT;
     static_assert(PSS_MAX_VOCAB <= (1u << 18), "ids of two 9-bit digits");
     const uint32_t tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
@@ -188,12 +190,12 @@ __device__ __forceinline__ bool pss_hist_finish(const pss_args& a, uint32_t row,
     const int hib = d ? 31 - (int)__clz(d) : 0;
     const int sh = hib >= 10 ? hib - 10 : 0;
     auto binof = [&](uint32_t k) -> uint32_t { return (k >> sh) & (PSS_HF_BINS - 1u); };
-    unsigned long long e[2];
-    uint32_t k[2];
-    bool v[2];
-    uint64_t q[2];
+    unsigned long long e[HR];
+    uint32_t k[HR];
+    bool v[HR];
+    uint64_t q[HR];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < HR; ++h) {
         const uint32_t i = tid + (uint32_t)h * NT;
         v[h] = i < n;
         e[h] = v[h] ? list[i] : 0ull;
@@ -212,7 +214,7 @@ __device__ __forceinline__ bool pss_hist_finish(const pss_args& a, uint32_t row,
     __syncthreads();
     /* 1 */
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < HR; ++h)
         if (v[h]) {
             atomicAdd(&hs.hc[binof(k[h])], 1u);
             atomicAdd((unsigned long long*)&hs.hq[binof(k[h])], (unsigned long long)q[h]);
@@ -253,7 +255,7 @@ __device__ __forceinline__ bool pss_hist_finish(const pss_args& a, uint32_t row,
         hs.aQK = (rK & 1u) ? S0q : S0q - q0;
     }
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < HR; ++h)
         if (v[h] && binof(k[h]) == bK) {
             const uint32_t pos = atomicAdd(&hs.bn[0], 1u);
             if (pos < PSS_HF_GATHER) hs.be[0][pos] = e[h];
@@ -293,7 +295,7 @@ __device__ __forceinline__ bool pss_hist_finish(const pss_args& a, uint32_t row,
         if (rP < rK) {
             if (rP >> 1 == tid) hs.aQP = (rP & 1u) ? S0q : S0q - q0;
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
+            for (int h = 0; h < HR; ++h)
                 if (v[h] && binof(k[h]) == bP) {
                     const uint32_t pos = atomicAdd(&hs.bn[1], 1u);
                     if (pos < PSS_HF_GATHER) hs.be[1][pos] = e[h];
@@ -318,12 +320,12 @@ __device__ __forceinline__ bool pss_hist_finish(const pss_args& a, uint32_t row,
         tau = hs.tauP > tau ? hs.tauP : tau;
     }
     /* 4 */
-    bool kp[2];
-    float p[2];
+    bool kp[HR];
+    float p[HR];
     uint64_t z = 0ull;
     uint32_t cnt = 0u, last = 0u;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < HR; ++h) {
         p[h] = pss_prob(pss_unkey(k[h]), tmax);
         kp[h] = v[h] && k[h] >= tau && (!c.useMinP || p[h] >= c.minP);
         z += kp[h] ? q[h] : 0ull;
@@ -340,7 +342,7 @@ __device__ __forceinline__ bool pss_hist_finish(const pss_args& a, uint32_t row,
     }
     /* 5, first pass (kept masses by the upper id digit) */
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < HR; ++h)
         if (kp[h]) atomicAdd((unsigned long long*)&hs.h8[0][(uint32_t)e[h] >> 9], (unsigned long long)q[h]);
     __syncthreads();
     uint64_t Z = 0ull;
@@ -352,7 +354,7 @@ __device__ __forceinline__ bool pss_hist_finish(const pss_args& a, uint32_t row,
         lastAll = hs.wl[x] > lastAll ? hs.wl[x] : lastAll;
     }
     uint32_t newRng;
-    const uint32_t u24 = pss_draw_u24(a, row, &newRng);
+    const uint32_t u24 = pss_draw_u24_pre(a.rng_mode, pre.rng, pre.step, row, &newRng);
     const uint64_t target = pss_draw_target(u24, Z);
     uint32_t tok, flags = 0;
     if (Z > 0) {
@@ -367,7 +369,7 @@ __device__ __forceinline__ bool pss_hist_finish(const pss_args& a, uint32_t row,
         __syncthreads();
         const uint32_t d1 = hs.d1;
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < HR; ++h)
             if (kp[h] && ((uint32_t)e[h] >> 9) == d1)
                 atomicAdd((unsigned long long*)&hs.h8[1][(uint32_t)e[h] & 511u], (unsigned long long)q[h]);
         __syncthreads();
@@ -393,7 +395,7 @@ __device__ __forceinline__ bool pss_hist_finish(const pss_args& a, uint32_t row,
         __syncthreads();
         const float zf = (float)Z * 0x1.0p-45f;
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < HR; ++h)
             if (kp[h]) {
                 const uint32_t id = (uint32_t)e[h];
                 if (a.kept_mask) atomicOr(&a.kept_mask[(size_t)row * a.mask_words + (id >> 5)], 1u << (id & 31u));
@@ -411,7 +413,7 @@ __device__ __forceinline__ bool pss_hist_finish(const pss_args& a, uint32_t row,
         inf.target = target;
         inf.u24 = u24;
         inf.flags = flags;
-        pss_epilogue(a, row, tok, false, c.W, newRng, inf);
+        pss_epilogue_pre(a, row, tok, false, c.W, newRng, inf, pre.pos, pre.step);
     }
     return true;
 }
@@ -470,6 +472,11 @@ __global__ void __launch_bounds__(PSS_WSP_NT) pss_wsplit_kernel(pss_args a, uint
     static_assert(PSS_MAX_PENALTY_LEN <= PSS_WSP_NT, "one window slot per thread");
     const uint32_t hid = tid < PSS_MAX_PENALTY_LEN ? a.history[(size_t)row * PSS_MAX_PENALTY_LEN + tid] : PSS_SENTINEL;
     sample_params sp = params[row];
+    /* the row state, for the finishing workgroup (written only by its epilogue) */
+    pss_row_pre pre;
+    pre.rng = a.rng[row];
+    pre.step = a.step[row];
+    pre.pos = a.position[row];
     __asm__ __volatile__("" ::: "memory");
     /* the row's waves of WSPAN ids, split evenly over the G segments (at
      * most 16 each); the resource covers the segment only, so loads beyond
@@ -723,24 +730,34 @@ __global__ void __launch_bounds__(PSS_WSP_NT) pss_wsplit_kernel(pss_args a, uint
     }
     bool general = !cov;
     if (!general) {
-        /* counts, offsets and the bound: every thread reads the G (<= 4)
-         * small values */
+        /* counts, bounds and candidates in one round trip: every thread
+         * reads the G (<= 4) counts and bounds and its share of each
+         * segment's whole staged range (entries beyond a count are dropped) */
         static_assert(PSS_MAX_VOCAB <= 4u * 65536u, "at most 4 segments");
-        uint32_t off[4];
-        uint32_t N = 0u, L2min = 0xFFFFFFFFu;
-        bool over = false;
+        constexpr int PS = (int)(PSS_WSP_SCAP / PSS_WSP_NT); /* entries per thread and segment */
+        constexpr int GR = 4 * PS;
+        const unsigned long long* rowpool = (const unsigned long long*)(ws + 1);
+        uint32_t ns[4];
+        uint32_t L2min = 0xFFFFFFFFu;
 #pragma unroll
         for (uint32_t s = 0; s < 4u; ++s) {
-            off[s] = N;
+            ns[s] = 0u;
             if (s < G) {
-                const uint32_t n = pss_ld_agent(&ws->seg_count[s]);
+                ns[s] = pss_ld_agent(&ws->seg_count[s]);
                 const uint32_t l2 = (uint32_t)pss_ld_agent64(&ws->seg_best[s]);
-                over |= n == PSS_SEG_OVERFLOW;
-                N += n == PSS_SEG_OVERFLOW ? 0u : n;
                 L2min = l2 < L2min ? l2 : L2min;
             }
         }
         const uint32_t B = pss_ld_agent(&ws->bound);
+        unsigned long long ev[GR];
+#pragma unroll
+        for (int r = 0; r < GR; ++r) {
+            const uint32_t sg = (uint32_t)(r / PS), i = (uint32_t)(r % PS) * PSS_WSP_NT + tid;
+            ev[r] = (sg < G && i < cap) ? pss_ld_agent64(rowpool + (size_t)sg * capg + i) : 0ull;
+        }
+        bool over = false;
+#pragma unroll
+        for (uint32_t s = 0; s < 4u; ++s) over |= s < G && ns[s] == PSS_SEG_OVERFLOW;
         const uint32_t thr2 = B > L2min ? B : L2min;
         if (tid < 256u) sh.f.hist[0][tid] = sh.f.hist[1][tid] = 0u;
         if (tid == 0u) {
@@ -751,29 +768,13 @@ __global__ void __launch_bounds__(PSS_WSP_NT) pss_wsplit_kernel(pss_args a, uint
         __syncthreads();
         general = over;
         if (!general) {
-            /* every entry requested before any is used (one round trip);
-             * N <= 4 segments x PSS_WSP_SCAP */
-            constexpr int GR = (int)(4u * PSS_WSP_SCAP / PSS_WSP_NT);
-            const unsigned long long* rowpool = (const unsigned long long*)(ws + 1);
-            unsigned long long ev[GR];
-#pragma unroll
-            for (int r = 0; r < GR; ++r) {
-                const uint32_t i = (uint32_t)r * PSS_WSP_NT + tid;
-                uint32_t s = 0u, os = 0u;
-#pragma unroll
-                for (uint32_t q = 1; q < 4u; ++q)
-                    if (q < G && i >= off[q]) {
-                        s = q;
-                        os = off[q];
-                    }
-                ev[r] = i < N ? pss_ld_agent64(rowpool + (size_t)s * capg + (i - os)) : 0ull;
-            }
             uint32_t mk = 0u;
 #pragma unroll
             for (int r = 0; r < GR; ++r) {
-                if ((uint32_t)r * PSS_WSP_NT >= N) break;
+                const uint32_t sg = (uint32_t)(r / PS), i = (uint32_t)(r % PS) * PSS_WSP_NT + tid;
+                if (sg >= G) break;
                 const unsigned long long e = ev[r];
-                const bool keep = (uint32_t)r * PSS_WSP_NT + tid < N && (uint32_t)(e >> 32) >= thr2;
+                const bool keep = i < ns[sg] && (uint32_t)(e >> 32) >= thr2;
                 const uint64_t m = __ballot(keep);
                 if (m) {
                     uint32_t b0 = 0u;
@@ -792,15 +793,14 @@ __global__ void __launch_bounds__(PSS_WSP_NT) pss_wsplit_kernel(pss_args a, uint
             const uint32_t n = sh.f.nc;
             general = n > PSS_FIN_LIST_CAP || n == 0u;
             if (!general) {
-                pss_row_pre pre;
-                pre.rng = a.rng[row];
-                pre.step = a.step[row];
-                pre.pos = a.position[row];
+                pss_pin_s(pre.rng);
+                pss_pin_s(pre.step);
+                pss_pin_s(pre.pos);
                 if (!pss_list_finish_fast<PSS_WSP_NT>(a, row, c, sh.list, n, thr2, pre, sh.f, true)) {
                     uint32_t tmaxKey = 0u;
 #pragma unroll
                     for (int v = 0; v < PSS_WSP_NW; ++v) tmaxKey = sh.f.mx[v] > tmaxKey ? sh.f.mx[v] : tmaxKey;
-                    if (n > PSS_HF_N || !pss_hist_finish(a, row, c, sh.list, n, thr2, tmaxKey, S.f.u.hs))
+                    if (n > PSS_HF_N || !pss_hist_finish(a, row, c, sh.list, n, thr2, tmaxKey, pre, S.f.u.hs))
                         pss_list_finish<PSS_WSP_NT>(a, row, c, sh.list, n, sh.f.g, thr2);
                 }
             }
