@@ -209,8 +209,10 @@ __global__ void __launch_bounds__(PSS_RES_NT) pss_res_kernel(pss_args a, const s
     }
 
     /* 3. the loads in arrival order */
-    /* maxima each wave publishes: 16 x 8 >= K for K <= 128, 16 x 16 up to 256 */
-    const uint32_t npub = c.K <= 128u ? 8u : 16u;
+    /* maxima each wave publishes: 16 x 8 for K <= 64, 16 x 16 up to 256 (at
+     * least 2 K of them above 64, so that the K-th largest published value
+     * stays close to the K-th largest lane maximum) */
+    const uint32_t npub = c.K <= 64u ? 8u : 16u;
     float m = NEG_INF, m2 = NEG_INF;
     uint32_t mpos = 0u;
     uint64_t best = 0ull;
@@ -439,7 +441,11 @@ __global__ void __launch_bounds__(PSS_RES_NT) pss_res_kernel(pss_args a, const s
         pss_general_row<PSS_RES_NT>(a, row, f.g, S.winbits, Gm::BW);
         return;
     }
-    if (!pss_list_finish_fast<PSS_RES_NT>(a, row, c, f.cl, n, G, pre, f, true))
+    /* the fp32 kernel finishes 65..256 candidates with the radix passes and
+     * the one-wave tail: with the two-wave sort tail inlined as well, its
+     * streaming code compiled differently and the headline step took 1.7 us
+     * longer (24.6 -> 26.4 us, measured A/B), more than such rows gain */
+    if (!pss_list_finish_fast<PSS_RES_NT, DT == PSS_DTYPE_F16>(a, row, c, f.cl, n, G, pre, f, true))
         pss_list_finish<PSS_RES_NT>(a, row, c, f.cl, n, f.g, G);
 }
 

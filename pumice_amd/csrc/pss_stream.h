@@ -817,9 +817,10 @@ __device__ __forceinline__ void pss_tail256_2w(const pss_args& a, uint32_t row, 
  * or ties), wave 0 finishes with pss_wave_tail4 instead of step 3.  Returns
  * false (nothing written) for K > PSS_SEG_KMAX, more than PSS_FAST_N
  * candidates, or more than PSS_KEPT_CAP entries at or above the K-th largest
- * (heavy ties).
+ * (heavy ties).  T256: 65..256 entries after the compaction go to
+ * pss_tail256_2w (no radix passes).
  */
-template <int NT>
+template <int NT, bool T256 = true>
 __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t row,
                                                      const pss_rowcfg& c, const unsigned long long* list,
                                                      uint32_t n, uint32_t G, const pss_row_pre& pre,
@@ -862,7 +863,7 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
     uint32_t tauK = 0u, cnt = nc;
     bool coarse = false; /* tauK is a floor below the K-th largest (at most 64 entries at or above it) */
     const unsigned long long* src = cl;
-    if (nc > 64u && nc <= 256u) {
+    if (T256 && nc > 64u && nc <= 256u) {
         /* 65..256 candidates: two waves sort them all (no radix passes) */
         if (tid < 128) pss_tail256_2w(a, row, c, cl, nc, pre, u24, newRng, sh);
         return true;
