@@ -27,6 +27,8 @@
 
 #include "pss_device.h"
 
+#include <type_traits>
+
 #define PSS_GEN_NT 1024
 #define PSS_GEN_U 8 /* ids per thread per pass step, loads requested together */
 #define PSS_NO_TOKEN 0xFFFFFFFFu
@@ -251,45 +253,60 @@ __device__ __forceinline__ void pss_general_row(const pss_args& a, uint32_t row,
         /* 16-byte aligned rows: the block as 16-byte loads, all in flight
          * at once (4 per lane fp32, 2 fp16; lane l on 4 (8) consecutive ids) */
         const bool vec = a.vec_ok && (V * (uint32_t)esz) % 16u == 0u;
-        for (uint32_t b = wv; b < nblk && vec; b += NWV) {
-            constexpr int NQ = 4;
-            const uint32_t per = a.dtype == PSS_DTYPE_F16 ? 8u : 4u; /* ids per 16-byte load */
-            const uint32_t nq = 1024u / (64u * per);                 /* loads per lane: 4 or 2 */
-            uint4 r[NQ];
+        /* specialized on the element width and on whether the row has a
+         * window (V is a multiple of the ids per 16-byte load, so a load is
+         * all in the row or all past it) */
+        auto blocks = [&](auto PER, auto PEN) {
+            constexpr uint32_t per = decltype(PER)::value; /* ids per 16-byte load: 4 fp32, 8 fp16 */
+            constexpr bool pen = decltype(PEN)::value;
+            constexpr int nq = (int)(1024u / (64u * per)); /* loads per lane: 4 or 2 */
+            uint32_t kmin = 0xFFFFFFFFu;
+            for (uint32_t b = wv; b < nblk; b += NWV) {
+                uint4 r[nq];
 #pragma unroll
-            for (int q = 0; q < NQ; ++q) {
-                const uint32_t j = b * 1024u + (uint32_t)q * 64u * per + lane * per;
-                r[q] = (uint32_t)q < nq && j < V ? *(const uint4*)((const char*)rowp + (size_t)j * esz)
-                                                 : make_uint4(0u, 0u, 0u, 0u);
-            }
-            uint32_t km = 0u, cm = 0u;
+                for (int q = 0; q < nq; ++q) {
+                    const uint32_t j = b * 1024u + (uint32_t)q * 64u * per + lane * per;
+                    r[q] = j < V ? *(const uint4*)((const char*)rowp + (size_t)j * esz) : make_uint4(0u, 0u, 0u, 0u);
+                }
+                uint32_t km = 0u, cm = 0u;
 #pragma unroll
-            for (int q = 0; q < NQ; ++q) {
-                const uint32_t w[4] = {r[q].x, r[q].y, r[q].z, r[q].w};
+                for (int q = 0; q < nq; ++q) {
+                    const uint32_t j0 = b * 1024u + (uint32_t)q * 64u * per + lane * per;
+                    if (j0 >= V) continue;
+                    const uint32_t w[4] = {r[q].x, r[q].y, r[q].z, r[q].w};
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const uint32_t j = b * 1024u + (uint32_t)q * 64u * per + lane * per + (uint32_t)e;
-                    if ((uint32_t)q < nq && (uint32_t)e < per && j < V) {
+                    for (uint32_t e = 0; e < per; ++e) {
                         float x;
-                        if (a.dtype == PSS_DTYPE_F16) {
-                            const uint16_t h = (uint16_t)(w[e >> 1] >> ((e & 1) * 16));
+                        if (per == 8u) {
+                            const uint16_t h = (uint16_t)(w[e >> 1] >> ((e & 1u) * 16u));
                             _Float16 hf;
                             __builtin_memcpy(&hf, &h, 2);
                             x = (float)hf;
                         } else {
-                            x = __uint_as_float(w[e & 3]);
+                            x = __uint_as_float(w[e & 3u]);
                         }
-                        const uint32_t k = pss_key(pss_transform(x, c.doPen && pss_bit(bits, j), c));
+                        const uint32_t k = pss_key(pss_transform(x, pen && pss_bit(bits, j0 + e), c));
                         cm = k > km ? 1u : cm + (k == km ? 1u : 0u);
                         km = k > km ? k : km;
-                        nk = (0xFFFFFFFFull ^ k) > nk ? (0xFFFFFFFFull ^ k) : nk;
+                        kmin = k < kmin ? k : kmin;
                     }
                 }
+                mk = km > mk ? km : mk;
+                const uint32_t M = wave_max_u32(km);
+                const uint32_t cnt = wave_sum_u32(km == M ? cm : 0u);
+                if (lane == 0u) sh.hist[b] = ((uint64_t)M << 32) | cnt;
             }
-            mk = km > mk ? km : mk;
-            const uint32_t M = wave_max_u32(km);
-            const uint32_t cnt = wave_sum_u32(km == M ? cm : 0u);
-            if (lane == 0u) sh.hist[b] = ((uint64_t)M << 32) | cnt;
+            nk = (0xFFFFFFFFull ^ kmin) > nk ? (0xFFFFFFFFull ^ kmin) : nk;
+        };
+        if (vec) {
+            using f16w = std::integral_constant<uint32_t, 8u>;
+            using f32w = std::integral_constant<uint32_t, 4u>;
+            using penw = std::integral_constant<bool, true>;
+            using nopw = std::integral_constant<bool, false>;
+            if (a.dtype == PSS_DTYPE_F16)
+                c.doPen ? blocks(f16w{}, penw{}) : blocks(f16w{}, nopw{});
+            else
+                c.doPen ? blocks(f32w{}, penw{}) : blocks(f32w{}, nopw{});
         }
         for (uint32_t b = wv; b < nblk && !vec; b += NWV) {
             uint32_t km = 0u, cm = 0u;
