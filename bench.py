@@ -488,7 +488,7 @@ def main():
                     help="also run device-to-device copies of one headline batch (traffic calibration)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="no GPU: turn two rocprofv3 --pmc output directories into "
-                         "profiles/traffic_headline.json and exit")
+                         "profiles/sampler_traffic_by_config.md and exit")
     args = ap.parse_args()
     if args.traffic_from:
         traffic_from_pmc(args.traffic_from[0], args.traffic_from[1], os.path.join(ROOT, "profiles", TRAFFIC_MD))
