@@ -1192,7 +1192,8 @@ struct pss_wave_run {
  * restrict argument: the kernel's stores cannot alias it, so the row
  * parameters of later items still come through scalar loads.
  */
-template <int EPT, int DT, bool M1, bool FUSED, bool SMALL = false, bool WL = false, class RL = pss_row_lds>
+template <int EPT, int DT, bool M1, bool FUSED, bool SMALL = false, bool WL = false, class RL = pss_row_lds,
+          int NWT = PSS_SEG_NW>
 __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, uint32_t i0, uint32_t i1,
                                                const sample_params* __restrict__ params,
                                                pss_wave_lds<EPT, DT>* lds, unsigned long long* joint,
@@ -1200,7 +1201,7 @@ __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, u
     using Gm = pss_wgeom<EPT, DT>;
     constexpr int E = Gm::E, NL = Gm::NL;
     constexpr uint32_t ITEM = Gm::ITEM;
-    constexpr uint32_t NW = PSS_SEG_NW;
+    constexpr uint32_t NW = (uint32_t)NWT;
     constexpr uint32_t esz = DT == PSS_DTYPE_F16 ? 2u : 4u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(pss_tid() >> 6);
     const uint32_t lane = pss_tid() & 63u;
@@ -1808,8 +1809,9 @@ __global__ void __launch_bounds__(PSS_ST_NT) pss_fin_kernel(pss_args a, uint32_t
 /*
  * Small-batch form: GW workgroups per row (grid rows x GW), workgroup g of a
  * row takes items [g NS / GW, (g + 1) NS / GW) of that row only, at most
- * PSS_SEG_NW, in one round (each wave one item, the joint certificate over
- * the workgroup's items).  Pool entries and counts are agent-scope stores;
+ * NWS (16 waves, or 4 when the grid of four-wave workgroups fits one per CU:
+ * the row then spreads over 13 CUs at batch 1 instead of 4), in one round
+ * (each wave one item, the joint certificate over the workgroup's items).  Pool entries and counts are agent-scope stores;
  * every wave waits for its stores to complete, then the workgroup counts
  * itself on the row's ticket with an agent-scope acquire-release
  * fetch-add (release: this workgroup's stores happen before its count;
@@ -1827,9 +1829,9 @@ union pss_small_scratch {
     } fin;
 };
 
-template <int EPT, int DT, bool M1>
-__global__ void __launch_bounds__(PSS_SEG_NT) pss_small_kernel(pss_args a, uint32_t NS, uint32_t GW,
-                                                               const sample_params* __restrict__ params) {
+template <int EPT, int DT, bool M1, int NWS = PSS_SEG_NW>
+__global__ void __launch_bounds__(NWS * PSS_WAVE) pss_small_kernel(pss_args a, uint32_t NS, uint32_t GW,
+                                                                   const sample_params* __restrict__ params) {
     __shared__ pss_small_scratch<EPT, DT> U;
     __shared__ unsigned long long joint[PSS_SEG_NW];
     __shared__ uint32_t last;
@@ -1838,7 +1840,8 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_small_kernel(pss_args a, uint3
     const uint32_t row = blockIdx.x / GW, g = blockIdx.x - row * GW;
     const uint32_t s0 = g * NS / GW, s1 = (g + 1u) * NS / GW;
     const uint32_t tid = pss_tid();
-    pss_seg_rounds<EPT, DT, M1, false, true>(a, NS, row * NS + s0, row * NS + s1, params, U.st, joint, (pss_row_lds*)nullptr);
+    pss_seg_rounds<EPT, DT, M1, false, true, false, pss_row_lds, NWS>(a, NS, row * NS + s0, row * NS + s1, params, U.st,
+                                                                      joint, (pss_row_lds*)nullptr);
     pss_wait_mem(); /* this wave's pool stores, counts and staged loads have completed */
     __syncthreads();
     if (tid == 0u) {
@@ -1852,7 +1855,7 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_small_kernel(pss_args a, uint3
     sample_params sp;
     pss_row_pre pre;
     pss_load_row_state(a, params, row, sp, pre);
-    pss_fin_row<PSS_SEG_NT>(a, sp, pre, row, NS, U.fin.fs, U.fin.bits, PSS_ROW_BITS);
+    pss_fin_row<NWS * PSS_WAVE>(a, sp, pre, row, NS, U.fin.fs, U.fin.bits, PSS_ROW_BITS);
 }
 
 /* ---------------------------------------------------------------------- */
@@ -1904,6 +1907,20 @@ static inline hipError_t pss_seg_launch(const pss_args& a, uint32_t NS, uint32_t
 enum { PSS_FORM_FUSED = 0, PSS_FORM_SMALL = 1, PSS_FORM_SPLIT = 2, PSS_FORM_RESIDENT = 3 };
 
 static inline uint32_t pss_small_gw(uint32_t NS) { return (NS + PSS_SEG_NW - 1u) / PSS_SEG_NW; }
+/* Workgroups of four waves: a row spread over four times as many CUs, for
+ * launches whose grid still fits one workgroup per CU (batch 1 to a few rows). */
+#define PSS_SMALL4_NW 4
+static inline uint32_t pss_small4_gw(uint32_t NS) { return (NS + PSS_SMALL4_NW - 1u) / PSS_SMALL4_NW; }
+static inline uint32_t pss_cu_count() {
+    static uint32_t cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+    if (dev < 64 && cache[dev]) return cache[dev];
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 0;
+    if (dev < 64) cache[dev] = (uint32_t)cus;
+    return (uint32_t)cus;
+}
 
 template <int EPT>
 static inline hipError_t pss_stream_go(const pss_args& a, uint32_t rows, uint32_t max_k, int form,
@@ -1914,6 +1931,24 @@ static inline hipError_t pss_stream_go(const pss_args& a, uint32_t rows, uint32_
     const bool m1 = max_k <= (uint32_t)PSS_WAVE;
     hipError_t e;
     if (form == PSS_FORM_SMALL) {
+        const uint32_t GW4 = pss_small4_gw(NS);
+        if ((uint64_t)rows * GW4 <= (uint64_t)pss_cu_count()) {
+            const dim3 grid(rows * GW4), block(PSS_SMALL4_NW * PSS_WAVE);
+            if (a.dtype == PSS_DTYPE_F16) {
+                if (m1)
+                    pss_small_kernel<EPT, PSS_DTYPE_F16, true, PSS_SMALL4_NW><<<grid, block, 0, st>>>(a, NS, GW4, a.params);
+                else
+                    pss_small_kernel<EPT, PSS_DTYPE_F16, false, PSS_SMALL4_NW><<<grid, block, 0, st>>>(a, NS, GW4, a.params);
+            } else {
+                if (m1)
+                    pss_small_kernel<EPT, PSS_DTYPE_F32, true, PSS_SMALL4_NW><<<grid, block, 0, st>>>(a, NS, GW4, a.params);
+                else
+                    pss_small_kernel<EPT, PSS_DTYPE_F32, false, PSS_SMALL4_NW><<<grid, block, 0, st>>>(a, NS, GW4, a.params);
+            }
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+            if (split_ev && (e = hipEventRecord(split_ev, st)) != hipSuccess) return e;
+            return hipSuccess;
+        }
         const uint32_t GW = pss_small_gw(NS);
         if ((uint64_t)rows * GW > 0x7FFFFFFFull) return hipErrorInvalidValue;
         const dim3 grid(rows * GW), block(PSS_SEG_NT);
