@@ -441,11 +441,11 @@ __global__ void __launch_bounds__(PSS_RES_NT) pss_res_kernel(pss_args a, const s
         pss_general_row<PSS_RES_NT>(a, row, f.g, S.winbits, Gm::BW);
         return;
     }
-    /* the fp32 kernel finishes 65..256 candidates with the radix passes and
-     * the one-wave tail: with the two-wave sort tail inlined as well, its
-     * streaming code compiled differently and the headline step took 1.7 us
-     * longer (24.6 -> 26.4 us, measured A/B), more than such rows gain */
-    if (!pss_list_finish_fast<PSS_RES_NT, DT == PSS_DTYPE_F16>(a, row, c, f.cl, n, G, pre, f, true))
+    /* the fp32 kernel sorts at most 128 candidates in its tail and takes the
+     * radix passes above: with the 256-entry sort tail inlined, its streaming
+     * code compiled differently and the headline step took 1.7 us longer
+     * (24.6 -> 26.4 us, measured A/B) */
+    if (!pss_list_finish_fast<PSS_RES_NT, DT == PSS_DTYPE_F16 ? 256 : 128>(a, row, c, f.cl, n, G, pre, f, true))
         pss_list_finish<PSS_RES_NT>(a, row, c, f.cl, n, f.g, G);
 }
 

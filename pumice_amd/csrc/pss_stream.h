@@ -594,15 +594,15 @@ __device__ __forceinline__ void pss_tail64_2w(const pss_args& a, uint32_t row, c
 }
 
 /* One compare-exchange stage (block KB, distance J) of an ascending bitonic
- * sort of 256 values, four per lane at positions 64 r + lane (r = 0..3):
+ * sort of 64 R values, R per lane at positions 64 r + lane (r = 0..R-1):
  * distances of 64 and more pair registers of the lane, smaller ones lanes
  * (DPP / permlane exchanges). */
-template <uint32_t KB, uint32_t J>
-__device__ __forceinline__ void pss_sort256_stage(uint32_t (&x)[4], uint32_t lane) {
+template <int R, uint32_t KB, uint32_t J>
+__device__ __forceinline__ void pss_sortr_stage(uint32_t (&x)[R], uint32_t lane) {
     if constexpr (J >= 64u) {
         constexpr uint32_t d = J / 64u;
 #pragma unroll
-        for (uint32_t r = 0; r < 4u; ++r) {
+        for (uint32_t r = 0; r < (uint32_t)R; ++r) {
             if (r & d) continue;
             const uint32_t p = 64u * r + lane;
             const bool asc = (p & KB) == 0u;
@@ -613,7 +613,7 @@ __device__ __forceinline__ void pss_sort256_stage(uint32_t (&x)[4], uint32_t lan
     } else {
         const bool low = (lane & J) == 0u;
 #pragma unroll
-        for (uint32_t r = 0; r < 4u; ++r) {
+        for (uint32_t r = 0; r < (uint32_t)R; ++r) {
             const uint32_t p = 64u * r + lane;
             const bool asc = (p & KB) == 0u;
             const uint32_t y = lane_xor<(int)J>(x[r]);
@@ -621,28 +621,33 @@ __device__ __forceinline__ void pss_sort256_stage(uint32_t (&x)[4], uint32_t lan
         }
     }
 }
-template <uint32_t KB, uint32_t J>
-__device__ __forceinline__ void pss_sort256_from(uint32_t (&x)[4], uint32_t lane) {
-    pss_sort256_stage<KB, J>(x, lane);
+template <int R, uint32_t KB, uint32_t J>
+__device__ __forceinline__ void pss_sortr_from(uint32_t (&x)[R], uint32_t lane) {
+    pss_sortr_stage<R, KB, J>(x, lane);
     if constexpr (J > 1u)
-        pss_sort256_from<KB, J / 2u>(x, lane);
-    else if constexpr (KB < 256u)
-        pss_sort256_from<KB * 2u, KB>(x, lane);
+        pss_sortr_from<R, KB, J / 2u>(x, lane);
+    else if constexpr (KB < 64u * (uint32_t)R)
+        pss_sortr_from<R, KB * 2u, KB>(x, lane);
 }
 /* x[r] of position p (p uniform). */
-__device__ __forceinline__ uint32_t pss_pos256(const uint32_t (&x)[4], uint32_t p) {
+template <int R>
+__device__ __forceinline__ uint32_t pss_posr(const uint32_t (&x)[R], uint32_t p) {
     const uint32_t r = p >> 6, l = p & 63u;
-    const uint32_t v0 = wave_read_u32(x[0], l), v1 = wave_read_u32(x[1], l), v2 = wave_read_u32(x[2], l),
-                   v3 = wave_read_u32(x[3], l);
-    return r == 0u ? v0 : (r == 1u ? v1 : (r == 2u ? v2 : v3));
+    uint32_t v = wave_read_u32(x[0], l);
+#pragma unroll
+    for (int i = 1; i < R; ++i) {
+        const uint32_t vi = wave_read_u32(x[i], l);
+        v = r == (uint32_t)i ? vi : v;
+    }
+    return v;
 }
 
 /*
- * Finisher tail for 65..256 entries (src, in LDS) holding every element at
- * or above the K-th largest, run by waves 0 and 1 together (threads
- * 0..127), four entries per lane in each (positions 64 r + lane), as
+ * Finisher tail for 65..64 R entries (src, in LDS; R = 2 or 4) holding every
+ * element at or above the K-th largest, run by waves 0 and 1 together
+ * (threads 0..127), R entries per lane in each (positions 64 r + lane), as
  * pss_tail64_2w:
- *   wave 0: the keys sorted in descending order (one 256-value bitonic
+ *   wave 0: the keys sorted in descending order (one 64 R-value bitonic
  *     network in registers and lanes) give the K-th largest at position
  *     K - 1 and the key-order mass scan for the top-p cut; it hands the cut
  *     (with Z_k) to wave 1 through sh and ends;
@@ -653,30 +658,31 @@ __device__ __forceinline__ uint32_t pss_pos256(const uint32_t (&x)[4], uint32_t 
  *     the epilogue.
  * sh.hflag must be zero on entry (cleared before the caller's last barrier).
  */
-__device__ __forceinline__ void pss_tail256_2w(const pss_args& a, uint32_t row, const pss_rowcfg& c,
-                                               const unsigned long long* src, uint32_t cnt, const pss_row_pre& pre,
-                                               uint32_t u24, uint32_t newRng, pss_fin_small& sh) {
+template <int R>
+__device__ __forceinline__ void pss_tailr_2w(const pss_args& a, uint32_t row, const pss_rowcfg& c,
+                                             const unsigned long long* src, uint32_t cnt, const pss_row_pre& pre,
+                                             uint32_t u24, uint32_t newRng, pss_fin_small& sh) {
     static_assert(PSS_MAX_VOCAB <= (1u << 24), "ids and an 8-bit index in 32 bits");
     const uint32_t lane = threadIdx.x & 63u;
     if (threadIdx.x < 64u) {
-        uint32_t x[4];
+        uint32_t x[R];
 #pragma unroll
-        for (uint32_t r = 0; r < 4u; ++r) {
+        for (uint32_t r = 0; r < (uint32_t)R; ++r) {
             const uint32_t i = 64u * r + lane;
             x[r] = i < cnt ? ~(uint32_t)(src[i] >> 32) : 0xFFFFFFFFu; /* missing entries sort last as key 0 */
         }
-        pss_sort256_from<2u, 1u>(x, lane);
-        uint32_t sk[4];
+        pss_sortr_from<R, 2u, 1u>(x, lane);
+        uint32_t sk[R];
 #pragma unroll
-        for (uint32_t r = 0; r < 4u; ++r) sk[r] = ~x[r];
+        for (uint32_t r = 0; r < (uint32_t)R; ++r) sk[r] = ~x[r];
         const uint32_t tmaxKey = wave_read_u32(sk[0], 0u);
-        const uint32_t tauK = pss_pos256(sk, (c.K <= cnt ? c.K : cnt) - 1u);
+        const uint32_t tauK = pss_posr<R>(sk, (c.K <= cnt ? c.K : cnt) - 1u);
         const float tmax = pss_unkey(tmaxKey);
-        uint64_t P[4];
-        bool sv[4];
+        uint64_t P[R];
+        bool sv[R];
         uint64_t run = 0u;
 #pragma unroll
-        for (uint32_t r = 0; r < 4u; ++r) {
+        for (uint32_t r = 0; r < (uint32_t)R; ++r) {
             sv[r] = 64u * r + lane < cnt && sk[r] >= tauK;
             const uint64_t q = sv[r] ? pss_fixq(pss_prob(pss_unkey(sk[r]), tmax)) : 0ull;
             const uint64_t inc = wave_incl_scan_u64(q);
@@ -689,11 +695,11 @@ __device__ __forceinline__ void pss_tail256_2w(const pss_args& a, uint32_t row, 
             const uint64_t need = pss_topp_need(c.topP, zk);
             uint32_t pos = 0xFFFFFFFFu;
 #pragma unroll
-            for (int r = 3; r >= 0; --r) {
+            for (int r = R - 1; r >= 0; --r) {
                 const uint64_t m = __ballot(sv[r] && P[r] >= need);
                 if (m) pos = 64u * (uint32_t)r + (uint32_t)__ffsll((long long)m) - 1u;
             }
-            const uint32_t tauP = pos != 0xFFFFFFFFu ? pss_pos256(sk, pos) : tmaxKey;
+            const uint32_t tauP = pos != 0xFFFFFFFFu ? pss_posr<R>(sk, pos) : tmaxKey;
             tau = tauP > tau ? tauP : tau;
         }
         if (lane == 0u) {
@@ -705,10 +711,10 @@ __device__ __forceinline__ void pss_tail256_2w(const pss_args& a, uint32_t row, 
         return;
     }
     /* wave 1: the entries in id order with their keys and masses */
-    uint32_t ix[4];
+    uint32_t ix[R];
     uint32_t mk = 0u;
 #pragma unroll
-    for (uint32_t r = 0; r < 4u; ++r) {
+    for (uint32_t r = 0; r < (uint32_t)R; ++r) {
         const uint32_t i = 64u * r + lane;
         const unsigned long long e = i < cnt ? src[i] : 0ull;
         ix[r] = i < cnt ? (((uint32_t)e << 8) | i) : 0xFFFFFFFFu;
@@ -716,13 +722,13 @@ __device__ __forceinline__ void pss_tail256_2w(const pss_args& a, uint32_t row, 
         mk = i < cnt && k > mk ? k : mk;
     }
     const uint32_t tmaxKey = __builtin_amdgcn_readfirstlane(wave_max_u32(mk));
-    pss_sort256_from<2u, 1u>(ix, lane);
+    pss_sortr_from<R, 2u, 1u>(ix, lane);
     const float tmax = pss_unkey(tmaxKey);
-    uint32_t ik[4];
-    float ip[4];
-    uint64_t iq[4];
+    uint32_t ik[R];
+    float ip[R];
+    uint64_t iq[R];
 #pragma unroll
-    for (uint32_t r = 0; r < 4u; ++r) {
+    for (uint32_t r = 0; r < (uint32_t)R; ++r) {
         const bool iv = ix[r] != 0xFFFFFFFFu;
         ik[r] = iv ? (uint32_t)(src[ix[r] & 255u] >> 32) : 0u;
         ip[r] = iv ? pss_prob(pss_unkey(ik[r]), tmax) : 0.0f;
@@ -731,13 +737,13 @@ __device__ __forceinline__ void pss_tail256_2w(const pss_args& a, uint32_t row, 
     while (__hip_atomic_load(&sh.hflag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0u)
         __builtin_amdgcn_s_sleep(1);
     const uint32_t tau = sh.htau;
-    bool kp[4];
-    uint64_t C[4];
+    bool kp[R];
+    uint64_t C[R];
     uint64_t run = 0u;
     uint32_t keptCount = 0u;
     uint32_t lastPos = 0xFFFFFFFFu;
 #pragma unroll
-    for (uint32_t r = 0; r < 4u; ++r) {
+    for (uint32_t r = 0; r < (uint32_t)R; ++r) {
         kp[r] = ix[r] != 0xFFFFFFFFu && ik[r] >= tau && (!c.useMinP || ip[r] >= c.minP);
         const uint64_t inc = wave_incl_scan_u64(kp[r] ? iq[r] : 0ull);
         C[r] = run + inc;
@@ -750,16 +756,16 @@ __device__ __forceinline__ void pss_tail256_2w(const pss_args& a, uint32_t row, 
     const uint64_t target = pss_draw_target(u24, Z);
     uint32_t hitPos = 0xFFFFFFFFu;
 #pragma unroll
-    for (int r = 3; r >= 0; --r) {
+    for (int r = R - 1; r >= 0; --r) {
         const uint64_t m = __ballot(kp[r] && C[r] > target);
         if (m) hitPos = 64u * (uint32_t)r + (uint32_t)__ffsll((long long)m) - 1u;
     }
     uint32_t tok, flags = 0;
     if (hitPos != 0xFFFFFFFFu) {
-        tok = pss_pos256(ix, hitPos) >> 8;
+        tok = pss_posr<R>(ix, hitPos) >> 8;
     } else {
         /* the largest kept id (the last kept entry in id order) */
-        tok = lastPos != 0xFFFFFFFFu ? pss_pos256(ix, lastPos) >> 8 : 0u;
+        tok = lastPos != 0xFFFFFFFFu ? pss_posr<R>(ix, lastPos) >> 8 : 0u;
         flags |= PSS_INFO_FALLBACK;
     }
 
@@ -771,7 +777,7 @@ __device__ __forceinline__ void pss_tail256_2w(const pss_args& a, uint32_t row, 
             for (uint32_t j = lane; j < a.V; j += 64u) a.probs[(size_t)row * a.probs_stride + j] = 0.0f;
         pss_wait_mem();
 #pragma unroll
-        for (uint32_t r = 0; r < 4u; ++r)
+        for (uint32_t r = 0; r < (uint32_t)R; ++r)
             if (kp[r]) {
                 const uint32_t sid = ix[r] >> 8;
                 if (a.kept_mask) atomicOr(&a.kept_mask[(size_t)row * a.mask_words + (sid >> 5)], 1u << (sid & 31u));
@@ -817,10 +823,10 @@ __device__ __forceinline__ void pss_tail256_2w(const pss_args& a, uint32_t row, 
  * or ties), wave 0 finishes with pss_wave_tail4 instead of step 3.  Returns
  * false (nothing written) for K > PSS_SEG_KMAX, more than PSS_FAST_N
  * candidates, or more than PSS_KEPT_CAP entries at or above the K-th largest
- * (heavy ties).  T256: 65..256 entries after the compaction go to
- * pss_tail256_2w (no radix passes).
+ * (heavy ties).  TS (0, 128 or 256): 65..TS entries after the compaction go
+ * to the two-wave sort tail pss_tailr_2w (no radix passes).
  */
-template <int NT, bool T256 = true>
+template <int NT, int TS = 256>
 __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t row,
                                                      const pss_rowcfg& c, const unsigned long long* list,
                                                      uint32_t n, uint32_t G, const pss_row_pre& pre,
@@ -863,9 +869,9 @@ __device__ __forceinline__ bool pss_list_finish_fast(const pss_args& a, uint32_t
     uint32_t tauK = 0u, cnt = nc;
     bool coarse = false; /* tauK is a floor below the K-th largest (at most 64 entries at or above it) */
     const unsigned long long* src = cl;
-    if (T256 && nc > 64u && nc <= 256u) {
-        /* 65..256 candidates: two waves sort them all (no radix passes) */
-        if (tid < 128) pss_tail256_2w(a, row, c, cl, nc, pre, u24, newRng, sh);
+    if (TS > 0 && nc > 64u && nc <= (uint32_t)TS) {
+        /* 65..TS candidates: two waves sort them all (no radix passes) */
+        if (tid < 128) pss_tailr_2w<(TS > 0 ? TS / 64 : 1)>(a, row, c, cl, nc, pre, u24, newRng, sh);
         return true;
     }
     if (nc > 64u) {
