@@ -1666,7 +1666,7 @@ __global__ void __launch_bounds__(PSS_SEG_NT) pss_row_kernel(pss_args a, uint32_
 /* Finish row `row` from its NS items in the workspace (all NT threads of the
  * workgroup; candidates gathered into sh.list).  Everything the finish needs
  * is requested in one round trip before anything is waited for: thread s < NS
- * loads item s's count, its greedy best and the first PSS_FIN_SPEC entries
+ * loads item s's count, its greedy best and the first SPEC (PSS_FIN_SPEC or twice it) entries
  * of its pool range (one 128-byte line; an item rarely has more, the rest
  * follow in a second trip), every thread the row-wide bound G; the row's
  * parameters and state come loaded by the caller.  Of the first PSS_FIN_SPEC
@@ -1688,12 +1688,12 @@ __device__ __forceinline__ void pss_load_row_state(const pss_args& a, const samp
     pre.pos = a.position[row + z];
     sp = params[row];
 }
-template <int NT>
+template <int NT, uint32_t SPEC = PSS_FIN_SPEC>
 __device__ __forceinline__ void pss_fin_row(const pss_args& a, const sample_params& sp, const pss_row_pre& pre_in,
                                             uint32_t row, uint32_t NS, pss_fin_shared& sh, uint32_t* bits,
                                             uint32_t bit_words) {
     static_assert(NT >= PSS_SEG_MAX_SLOTS, "one thread per item");
-    static_assert(PSS_FIN_SPEC == 16u, "one 128-byte line per item");
+    static_assert(SPEC == 16u || SPEC == 32u, "one or two 128-byte lines per item");
     const uint32_t tid = pss_tid();
     pss_row_ws* ws = (pss_row_ws*)((char*)a.ws + (size_t)row * PSS_WS_ROW_BYTES);
     const uint32_t capw = pss_pool_capw(NS);
@@ -1709,9 +1709,9 @@ __device__ __forceinline__ void pss_fin_row(const pss_args& a, const sample_para
         ns = pss_ld_agent(&ws->seg_count[tid]);
         best = pss_ld_agent64(&ws->seg_best[tid]);
     }
-    unsigned long long v[PSS_FIN_SPEC];
+    unsigned long long v[SPEC];
 #pragma unroll
-    for (int j = 0; j < (int)PSS_FIN_SPEC / 2; ++j) {
+    for (int j = 0; j < (int)SPEC / 2; ++j) {
         const uint4 w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(prs, (int)(voff + 16u * j), 0, PSS_SC1));
         v[2 * j] = ((unsigned long long)w.y << 32) | w.x;
         v[2 * j + 1] = ((unsigned long long)w.w << 32) | w.z;
@@ -1738,9 +1738,9 @@ __device__ __forceinline__ void pss_fin_row(const pss_args& a, const sample_para
         const uint32_t n0 = over ? 0u : ns;
         uint32_t keep = 0u;
 #pragma unroll
-        for (uint32_t u = 0; u < PSS_FIN_SPEC; ++u)
+        for (uint32_t u = 0; u < SPEC; ++u)
             keep |= (u < n0 && (uint32_t)(v[u] >> 32) >= G) ? 1u << u : 0u;
-        const uint32_t extra = n0 > PSS_FIN_SPEC ? n0 - PSS_FIN_SPEC : 0u;
+        const uint32_t extra = n0 > SPEC ? n0 - SPEC : 0u;
         /* (overflowed items << 54) | (entries not filtered << 32) | entries
          * written: sums of at most 256 items stay within their fields */
         const uint64_t mine = over ? (1ull << 54) : (((uint64_t)extra << 32) | (uint64_t)(__popc(keep) + extra));
@@ -1763,9 +1763,9 @@ __device__ __forceinline__ void pss_fin_row(const pss_args& a, const sample_para
         if (slot && (uint32_t)tot64 <= PSS_FIN_LIST_CAP) {
             uint32_t o = off;
 #pragma unroll
-            for (uint32_t u = 0; u < PSS_FIN_SPEC; ++u)
+            for (uint32_t u = 0; u < SPEC; ++u)
                 if ((keep >> u) & 1u) sh.list[o++] = v[u];
-            for (uint32_t i0 = PSS_FIN_SPEC; i0 < n0; i0 += 8u) {
+            for (uint32_t i0 = SPEC; i0 < n0; i0 += 8u) {
                 unsigned long long w[8];
 #pragma unroll
                 for (int u = 0; u < 8; ++u) w[u] = i0 + u < n0 ? pss_ld_agent64(pool + (size_t)tid * capw + i0 + u) : 0ull;
@@ -1778,7 +1778,7 @@ __device__ __forceinline__ void pss_fin_row(const pss_args& a, const sample_para
          * histograms (both before the barrier) */
         uint32_t mk = 0u;
 #pragma unroll
-        for (uint32_t u = 0; u < PSS_FIN_SPEC; ++u)
+        for (uint32_t u = 0; u < SPEC; ++u)
             mk = ((keep >> u) & 1u) && (uint32_t)(v[u] >> 32) > mk ? (uint32_t)(v[u] >> 32) : mk;
         mk = wave_max_u32(mk);
         if ((tid & 63u) == 0u) sh.f.mx[tid >> 6] = mk;
@@ -1861,7 +1861,10 @@ __global__ void __launch_bounds__(NWS * PSS_WAVE) pss_small_kernel(pss_args a, u
     sample_params sp;
     pss_row_pre pre;
     pss_load_row_state(a, params, row, sp, pre);
-    pss_fin_row<NWS * PSS_WAVE>(a, sp, pre, row, NS, U.fin.fs, U.fin.bits, PSS_ROW_BITS);
+    /* four-wave workgroups certify over four items, so an item holds more
+     * candidates: two lines of each requested in the first round trip */
+    pss_fin_row<NWS * PSS_WAVE, NWS < PSS_SEG_NW ? 2u * PSS_FIN_SPEC : PSS_FIN_SPEC>(a, sp, pre, row, NS, U.fin.fs,
+                                                                                    U.fin.bits, PSS_ROW_BITS);
 }
 
 /* ---------------------------------------------------------------------- */
