@@ -178,9 +178,25 @@ __device__ __forceinline__ uint32_t pss_hf_digit512(const uint64_t* h, uint64_t&
  * for bit, as pss_list_finish.  Returns false (nothing written) when a bin
  * it must resolve holds more than 64 entries (dense ties).
  */
+/* The histogram finisher's bins and counters at their initial values (all
+ * threads; a barrier must follow before pss_hist_finish). */
+__device__ __forceinline__ void pss_hist_clear(pss_hfin_shared& hs) {
+    const uint32_t tid = threadIdx.x;
+    for (uint32_t i = tid; i < PSS_HF_BINS; i += PSS_WSP_NT) {
+        hs.hc[i] = 0u;
+        hs.hq[i] = 0ull;
+    }
+    for (uint32_t i = tid; i < 2u * 512u; i += PSS_WSP_NT) (&hs.h8[0][0])[i] = 0ull;
+    if (tid == 0u) {
+        hs.rK = hs.rP = 0xFFFFFFFFu;
+        hs.bn[0] = hs.bn[1] = 0u;
+    }
+}
+
 __device__ __forceinline__ bool pss_hist_finish(const pss_args& a, uint32_t row, const pss_rowcfg& c,
                                                 const unsigned long long* list, uint32_t n, uint32_t lo,
-                                                uint32_t tmaxKey, const pss_row_pre& pre, pss_hfin_shared& hs) {
+                                                uint32_t tmaxKey, const pss_row_pre& pre, pss_hfin_shared& hs,
+                                                bool cleared) {
     constexpr int HR = PSS_HF_R;
     constexpr int NT = PSS_WSP_NT;
     static_assert(PSS_MAX_VOCAB <= (1u << 18), "ids of two 9-bit digits");
@@ -193,6 +209,7 @@ __device__ __forceinline__ bool pss_hist_finish(const pss_args& a, uint32_t row,
     unsigned long long e[HR];
     uint32_t k[HR];
     bool v[HR];
+    float p[HR];
     uint64_t q[HR];
 #pragma unroll
     for (int h = 0; h < HR; ++h) {
@@ -200,18 +217,13 @@ __device__ __forceinline__ bool pss_hist_finish(const pss_args& a, uint32_t row,
         v[h] = i < n;
         e[h] = v[h] ? list[i] : 0ull;
         k[h] = (uint32_t)(e[h] >> 32);
-        q[h] = v[h] ? pss_fixq(pss_prob(pss_unkey(k[h]), tmax)) : 0ull;
+        p[h] = v[h] ? pss_prob(pss_unkey(k[h]), tmax) : 0.0f;
+        q[h] = v[h] ? pss_fixq(p[h]) : 0ull;
     }
-    for (uint32_t i = tid; i < PSS_HF_BINS; i += NT) {
-        hs.hc[i] = 0u;
-        hs.hq[i] = 0ull;
+    if (!cleared) {
+        pss_hist_clear(hs);
+        __syncthreads();
     }
-    for (uint32_t i = tid; i < 2u * 512u; i += NT) (&hs.h8[0][0])[i] = 0ull;
-    if (tid == 0u) {
-        hs.rK = hs.rP = 0xFFFFFFFFu;
-        hs.bn[0] = hs.bn[1] = 0u;
-    }
-    __syncthreads();
     /* 1 */
 #pragma unroll
     for (int h = 0; h < HR; ++h)
@@ -321,12 +333,10 @@ __device__ __forceinline__ bool pss_hist_finish(const pss_args& a, uint32_t row,
     }
     /* 4 */
     bool kp[HR];
-    float p[HR];
     uint64_t z = 0ull;
     uint32_t cnt = 0u, last = 0u;
 #pragma unroll
     for (int h = 0; h < HR; ++h) {
-        p[h] = pss_prob(pss_unkey(k[h]), tmax);
         kp[h] = v[h] && k[h] >= tau && (!c.useMinP || p[h] >= c.minP);
         z += kp[h] ? q[h] : 0ull;
         cnt += kp[h] ? 1u : 0u;
@@ -765,6 +775,10 @@ __global__ void __launch_bounds__(PSS_WSP_NT) pss_wsplit_kernel(pss_args a, uint
             sh.f.nk = 0u;
             sh.f.hflag = 0u;
         }
+        /* top-k above the fast finisher's: the histogram finisher's bins
+         * cleared under the same barrier */
+        const bool hf = c.K > PSS_SEG_KMAX;
+        if (hf) pss_hist_clear(S.f.u.hs);
         __syncthreads();
         general = over;
         if (!general) {
@@ -800,7 +814,7 @@ __global__ void __launch_bounds__(PSS_WSP_NT) pss_wsplit_kernel(pss_args a, uint
                     uint32_t tmaxKey = 0u;
 #pragma unroll
                     for (int v = 0; v < PSS_WSP_NW; ++v) tmaxKey = sh.f.mx[v] > tmaxKey ? sh.f.mx[v] : tmaxKey;
-                    if (n > PSS_HF_N || !pss_hist_finish(a, row, c, sh.list, n, thr2, tmaxKey, pre, S.f.u.hs))
+                    if (n > PSS_HF_N || !pss_hist_finish(a, row, c, sh.list, n, thr2, tmaxKey, pre, S.f.u.hs, hf))
                         pss_list_finish<PSS_WSP_NT>(a, row, c, sh.list, n, sh.f.g, thr2);
                 }
             }
