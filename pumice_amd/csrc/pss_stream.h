@@ -114,6 +114,7 @@ struct pss_fin_small {
     uint32_t nk;
     uint32_t fail;
     uint64_t gtot; /* finisher gather totals (overflowed, not filtered, entries) */
+    uint32_t g2;   /* finisher: the row bound after the small form's per-item maxima */
     /* two-wave tail: the key-order results wave 0 hands to wave 1 (hflag
      * is cleared with nk, before the caller's last barrier) */
     uint32_t hflag;
@@ -1203,7 +1204,7 @@ template <int EPT, int DT, bool M1, bool FUSED, bool SMALL = false, bool WL = fa
 __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, uint32_t i0, uint32_t i1,
                                                const sample_params* __restrict__ params,
                                                pss_wave_lds<EPT, DT>* lds, unsigned long long* joint,
-                                               RL* rl, const uint32_t* win = nullptr) {
+                                               RL* rl, const uint32_t* win = nullptr, bool top2 = false) {
     using Gm = pss_wgeom<EPT, DT>;
     constexpr int E = Gm::E, NL = Gm::NL;
     constexpr uint32_t ITEM = Gm::ITEM;
@@ -1428,6 +1429,16 @@ __device__ __forceinline__ void pss_seg_rounds(const pss_args& a, uint32_t NS, u
                 if (lane == 0u)
                     __hip_atomic_store(&joint[wave], ((unsigned long long)row << 32) | T, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_WORKGROUP);
+                if (SMALL && top2) {
+                    /* the item's two largest lane maxima (two distinct
+                     * elements), for the finishing workgroup's bound */
+                    const uint32_t lk = pss_key(pss_canon(run.top[0]));
+                    const uint32_t k1 = wave_max_u32(lk);
+                    const uint32_t first = (uint32_t)__builtin_ctzll(__ballot(lk == k1));
+                    const uint32_t k2 = wave_max_u32(lane == first ? 0u : lk);
+                    pss_row_ws* wsi = (pss_row_ws*)((char*)a.ws + (size_t)row * PSS_WS_ROW_BYTES);
+                    if (lane == 0u) pss_st_agent64(&wsi->seg_best[s], ((unsigned long long)k1 << 32) | k2);
+                }
             }
         } else if (ncov) {
             pss_wave_issue<EPT, DT, FUSED ? PSS_NT : 0>(a, nrow, ns, wl);
@@ -1688,7 +1699,7 @@ __device__ __forceinline__ void pss_load_row_state(const pss_args& a, const samp
     pre.pos = a.position[row + z];
     sp = params[row];
 }
-template <int NT, uint32_t SPEC = PSS_FIN_SPEC>
+template <int NT, uint32_t SPEC = PSS_FIN_SPEC, bool TOP2 = false>
 __device__ __forceinline__ void pss_fin_row(const pss_args& a, const sample_params& sp, const pss_row_pre& pre_in,
                                             uint32_t row, uint32_t NS, pss_fin_shared& sh, uint32_t* bits,
                                             uint32_t bit_words) {
@@ -1734,12 +1745,22 @@ __device__ __forceinline__ void pss_fin_row(const pss_args& a, const sample_para
     }
     bool general = !pss_seg_row_covered(a, sp);
     if (!general) {
+        /* TOP2 (small form, every item in wave 0): each item's slot holds its
+         * two largest lane maxima; the K-th largest of these (K <= 2 NS
+         * distinct elements) raises the row bound, usually to about the
+         * K-th largest itself */
+        uint32_t Gf = G;
+        if (TOP2 && NS <= (uint32_t)PSS_WAVE && c.K <= 2u * PSS_WAVE && tid < PSS_WAVE) {
+            const uint32_t v2[2] = {slot ? (uint32_t)(best >> 32) : 0u, slot ? (uint32_t)best : 0u};
+            const uint32_t x = wave_kth_largest<2, 24>(v2, c.K);
+            Gf = x > G ? x : G;
+        }
         const bool over = ns == PSS_SEG_OVERFLOW;
         const uint32_t n0 = over ? 0u : ns;
         uint32_t keep = 0u;
 #pragma unroll
         for (uint32_t u = 0; u < SPEC; ++u)
-            keep |= (u < n0 && (uint32_t)(v[u] >> 32) >= G) ? 1u << u : 0u;
+            keep |= (u < n0 && (uint32_t)(v[u] >> 32) >= Gf) ? 1u << u : 0u;
         const uint32_t extra = n0 > SPEC ? n0 - SPEC : 0u;
         /* (overflowed items << 54) | (entries not filtered << 32) | entries
          * written: sums of at most 256 items stay within their fields */
@@ -1783,16 +1804,20 @@ __device__ __forceinline__ void pss_fin_row(const pss_args& a, const sample_para
         mk = wave_max_u32(mk);
         if ((tid & 63u) == 0u) sh.f.mx[tid >> 6] = mk;
         if (tid < 256u) sh.f.hist[0][tid] = sh.f.hist[1][tid] = 0u;
-        if (tid == 0) sh.f.gtot = tot64;
+        if (tid == 0) {
+            sh.f.gtot = tot64;
+            sh.f.g2 = Gf;
+        }
         __syncthreads();
         tot64 = sh.f.gtot;
+        Gf = sh.f.g2;
         const uint32_t total = (uint32_t)tot64;
         const bool compacted = ((tot64 >> 32) & 0x3FFFFFu) == 0u;
         general = (tot64 >> 54) != 0u || total > PSS_FIN_LIST_CAP;
-        if (!general && !pss_list_finish_fast<NT>(a, row, c, sh.list, total, G, pre, sh.f, compacted)) {
+        if (!general && !pss_list_finish_fast<NT>(a, row, c, sh.list, total, Gf, pre, sh.f, compacted)) {
             /* slow path: candidates below the row-wide bound may remain in the
              * list; they are below the K-th largest and never selected */
-            pss_list_finish<NT>(a, row, c, sh.list, total, sh.f.g, G);
+            pss_list_finish<NT>(a, row, c, sh.list, total, sh.f.g, Gf);
         }
         if (tid == 0) pss_st_agent(&ws->bound, 0u); /* for the next launch */
     }
@@ -1847,7 +1872,7 @@ __global__ void __launch_bounds__(NWS * PSS_WAVE) pss_small_kernel(pss_args a, u
     const uint32_t s0 = g * NS / GW, s1 = (g + 1u) * NS / GW;
     const uint32_t tid = pss_tid();
     pss_seg_rounds<EPT, DT, M1, false, true, false, pss_row_lds, NWS>(a, NS, row * NS + s0, row * NS + s1, params, U.st,
-                                                                      joint, (pss_row_lds*)nullptr);
+                                                                      joint, (pss_row_lds*)nullptr, nullptr, true);
     pss_wait_mem(); /* this wave's pool stores, counts and staged loads have completed */
     __syncthreads();
     if (tid == 0u) {
@@ -1863,8 +1888,8 @@ __global__ void __launch_bounds__(NWS * PSS_WAVE) pss_small_kernel(pss_args a, u
     pss_load_row_state(a, params, row, sp, pre);
     /* four-wave workgroups certify over four items, so an item holds more
      * candidates: two lines of each requested in the first round trip */
-    pss_fin_row<NWS * PSS_WAVE, NWS < PSS_SEG_NW ? 2u * PSS_FIN_SPEC : PSS_FIN_SPEC>(a, sp, pre, row, NS, U.fin.fs,
-                                                                                    U.fin.bits, PSS_ROW_BITS);
+    pss_fin_row<NWS * PSS_WAVE, NWS < PSS_SEG_NW ? 2u * PSS_FIN_SPEC : PSS_FIN_SPEC, true>(
+        a, sp, pre, row, NS, U.fin.fs, U.fin.bits, PSS_ROW_BITS);
 }
 
 /* ---------------------------------------------------------------------- */
