@@ -471,7 +471,11 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    # an idle GPU runs the first few ms of launches about 5% slower while its
+    # clocks rise; 2,000 untimed launches (about 50 ms of the headline) reach
+    # the steady rate (200 timed launches: 25.0-25.6 us after 20 warmups,
+    # 23.8-24.0 us after 2,000, on one box)
+    ap.add_argument("--warmup", type=int, default=2000)
     ap.add_argument("--latency-steps", type=int, default=1000)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
