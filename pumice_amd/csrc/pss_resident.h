@@ -10,16 +10,16 @@
  * keeps PSS_RES_DEPTH loads in flight, the next one requested before each
  * wait (loads complete in issue order); no data passes through LDS.
  *
- * The first JC + 1 loads (three quarters of the row) stay in registers,
- * processed on arrival: t = l * (1/T), the window ids excluded (their
+ * The first JC + 1 loads (seven eighths of an fp32 row, three quarters of
+ * an fp16 row) stay in registers, processed on arrival: t = l * (1/T), the window ids excluded (their
  * penalized values enter the candidate list separately, once per distinct
  * id), each lane's running maximum.  Then every wave publishes the 8 (or 16)
  * largest of its lanes' maxima; after one barrier the K-th largest of all published values is a
  * certified lower bound G of the row's K-th largest value (K distinct
  * elements at or above it; ties are kept, so the bound is on values, not
- * positions).  From three quarters of the row G is close to the exact K-th
+ * positions).  From that much of the row G is close to the exact K-th
  * largest: the elements at or above it, from the registers at once and from
- * the last quarter as it arrives, go straight into the finisher's list
+ * the rest of the row as it arrives, go straight into the finisher's list
  * (about K + K/3 of them), and the row finishes after one more barrier in
  * one wave (pss_list_finish_fast of pss_stream.h): the exact K-th largest,
  * masses, top-p, min-p, the ascending-id draw and the epilogue.  The later
@@ -52,7 +52,11 @@ struct pss_res_geom {
     static constexpr uint32_t WSPAN = (uint32_t)NL * LSPAN;   /* ids per wave */
     static constexpr uint32_t VMAX = PSS_RES_NW * WSPAN;
     static constexpr uint32_t BW = (VMAX + 31u) / 32u;        /* window bitmap words */
-    static constexpr int JC = (3 * NL) / 4;                   /* loads 0..JC before the bound */
+    /* loads 0..JC before the bound: seven eighths of an fp32 row (23.9 ->
+     * 23.4 us at 256 x 102,400 against three quarters; no spills), three
+     * quarters of an fp16 row (seven eighths: 27.2 -> 27.7 us at 256 x
+     * 102,400 with top-k up to 100) */
+    static constexpr int JC = DT == PSS_DTYPE_F16 ? (3 * NL) / 4 : (7 * NL) / 8;
     /* loads a wave keeps in flight: a CU can have about 50 outstanding, so
      * more would stall the wave at its next request, ahead of the work on
      * the data that has arrived */
